@@ -1,0 +1,132 @@
+/*
+ * ondeviceinfer_wq.h - C ABI of the MI355X (gfx950) weight-only quantized Linear.
+ *
+ * These entry points replace the native calls behind OnDeviceInfer's pluggable
+ * compressed Linear (ondeviceinfer/weight_quantization/backend.py) and its
+ * INT8 explicit-dequant path (ondeviceinfer/quantized_model.py,
+ * ondeviceinfer/quantization.py).  Each declaration names the reference call
+ * it replaces.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer (hipMalloc'd or torch-owned) unless
+ *    noted; fp16 tensors are passed as uint16_t bit patterns; all tensors are
+ *    contiguous row-major.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Work is only
+ *    enqueued; nothing synchronises, nothing allocates.
+ *  - Return 0 (WQ_OK) or a WQ_ERR_* code; wq_last_error() then describes the
+ *    failure (thread-local, valid until the next failing call on the thread).
+ *  - Shapes: N output features, K input features, M activation rows.
+ */
+#ifndef ONDEVICEINFER_WQ_H
+#define ONDEVICEINFER_WQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WQ_OK 0
+#define WQ_ERR_INVALID_ARGUMENT 1 /* malformed shape / null pointer (Python: ValueError) */
+#define WQ_ERR_UNSUPPORTED 2      /* valid request this build does not implement (ValueError) */
+#define WQ_ERR_HIP 3              /* HIP runtime error (RuntimeError) */
+#define WQ_ERR_WORKSPACE 4        /* workspace too small (ValueError) */
+
+#define WQ_ABI_VERSION 1
+
+/* Error channel.  The reference raises Python exceptions directly
+ * (backend.py:174-175, :212-213, :229-230); the Python host maps codes back. */
+const char* wq_last_error(void);
+int wq_abi_version(void);
+
+/* ---------------------------------------------------------------- W4 (uint4, G-grouped) */
+
+/* Sizes of the gfx950 tile layout for an [n, k] pack-quantized weight.
+ * Requires n % 8 == 0, group_size % 128 == 0, k % group_size == 0.
+ * Replaces the allocation inside vllm gptq_marlin_repack (backend.py:214). */
+int wq_w4_repack_size(int64_t n, int64_t k, int64_t group_size,
+                      size_t* tiles_bytes, size_t* meta_bytes);
+
+/* One-time startup repack of compressed-tensors pack-quantized tensors:
+ *   weight_packed int32 [n, k/8] (8 codes per word along k, LSB first),
+ *   weight_scale  fp16  [n, k/group_size],
+ *   weight_zero_point int32 [n/8, k/group_size] (8 per word along n) or NULL
+ *   for the symmetric uint4b8 format (zero point 8)
+ * into `tiles` / `meta` (sizes from wq_w4_repack_size).
+ * Replaces vllm gptq_marlin_repack + marlin_permute_scales + unpack_unsigned/
+ * marlin_zero_points (backend.py:214-221). */
+int wq_w4_repack(const int32_t* weight_packed, const uint16_t* weight_scale,
+                 const int32_t* weight_zero_point, int64_t n, int64_t k, int64_t group_size,
+                 void* tiles, void* meta, void* stream);
+
+/* Exact inverse of wq_w4_repack (zero point words are 0x88888888 when the
+ * repack had none).  No reference counterpart: it proves the layout is
+ * lossless (the reference's own unpack is unpack_unsigned, backend.py:26-32). */
+int wq_w4_unpack(const void* tiles, const void* meta, int64_t n, int64_t k, int64_t group_size,
+                 int32_t* weight_packed, uint16_t* weight_scale, int32_t* weight_zero_point,
+                 void* stream);
+
+/* fp16 [n, k] = (q - z) * s read from the tile layout, with the same unpack
+ * arithmetic the W4A16 kernels use; equals decode_weight bit for bit
+ * (backend.py:41-54). */
+int wq_w4_dequant(const void* tiles, const void* meta, int64_t n, int64_t k, int64_t group_size,
+                  uint16_t* weight, void* stream);
+
+/* Explicit QDQ decode straight from compressed-tensors tensors, any group
+ * size and optional act-order g_idx (int32 [k] or NULL):
+ * fp16((q - z[g]) * scale[g]) computed in fp32, z = 8 when weight_zero_point is
+ * NULL.  weight_scale is fp32 [n, num_groups]; weight_zero_point is int32
+ * [ceil(n/8), num_groups]; g_idx entries must lie in [0, num_groups).
+ * Replaces decode_weight's W4
+ * branch (backend.py:41-54) for the reference_int4 backend. */
+int wq_w4_decode(const int32_t* weight_packed, const float* weight_scale,
+                 const int32_t* weight_zero_point, const int32_t* g_idx,
+                 int64_t n, int64_t k, int64_t num_groups, int64_t group_size,
+                 uint16_t* weight, void* stream);
+
+/* Workspace bytes wq_w4a16_linear needs for this shape (may be 0).
+ * Replaces marlin_make_workspace_new (backend.py:223). */
+int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t group_size, size_t* bytes);
+
+/* y fp16 [m, n] = x fp16 [m, k] . dequant(W)^T with fp32 accumulation.
+ * Dispatches on m: MFMA GEMV for small m, LDS-staged MFMA GEMM for large m.
+ * Replaces vllm gptq_marlin_gemm (backend.py:195-202, called from :233-248). */
+int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, const void* meta,
+                    int64_t n, int64_t group_size, uint16_t* y,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------- W8 (int8, per-output-channel scale) */
+
+/* fp16 [n, k] = fp16(q * scale[n]), scale fp32 [n].  Replaces the INT8 branch
+ * of decode_weight (backend.py:37-40), dequantize_linear_weight
+ * (quantization.py:320-330) and the scratch copy_+mul_ of
+ * int8_weight_only_linear (quantized_model.py:101-106). */
+int wq_w8_decode(const int8_t* qweight, const float* scale, int64_t n, int64_t k,
+                 uint16_t* weight, void* stream);
+
+/* y fp16 [m, n] = x fp16 [m, k] . (q * scale)^T (+ bias fp16 [n] or NULL),
+ * consuming the INT8 weight in its stored [n, k] row-major layout with no
+ * fp16 scratch (MFMA tiles when k % 128 == 0 and x, qweight are 16-byte
+ * aligned; a one-wave-per-output kernel otherwise).  Replaces the dequant + F.linear of
+ * int8_weight_only_linear (quantized_model.py:101-121) and quantized_linear
+ * (quantization.py:333-353). */
+int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight,
+                    const uint16_t* scale, int64_t n, const uint16_t* bias, uint16_t* y,
+                    void* stream);
+
+/* Symmetric per-output-channel INT8 quantizer: weight fp32 [n, k] ->
+ * qweight int8 [n, k] + fp16 scale [n] (absmax/127, zero rows scale 1,
+ * underflowing scales -> smallest fp16 subnormal, the stored scale divides,
+ * round-half-even, clamp +-127).  Non-finite input ORs bit 0 and a scale
+ * that overflows fp16 ORs bit 1 into *status_flags (device int32 that the
+ * caller zero-fills beforehand).  Replaces quantize_linear_weight
+ * (quantization.py:226-285). */
+int wq_w8_quantize(const float* weight, int64_t n, int64_t k, int8_t* qweight, uint16_t* scale,
+                   int32_t* status_flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONDEVICEINFER_WQ_H */

@@ -1,0 +1,300 @@
+"""ctypes binding of ``libondeviceinfer_wq.so`` (the C ABI in ``include/ondeviceinfer_wq.h``).
+
+torch is imported first so its bundled HIP runtime (``libamdhip64.so.7``) is
+the one the library binds to: the kernels then run in torch's context and on
+torch's streams.  The library is built in-tree by
+``python -m ondeviceinfer_amd.build``; if it is missing, every entry point
+raises instead of computing anything another way.
+
+The tensor-level helpers below validate dtype/shape/device/contiguity in
+Python (raising ``TypeError``/``ValueError`` like the reference), pass raw
+device pointers plus ``torch.cuda.current_stream()``, and map a nonzero status
+to an exception carrying ``wq_last_error()``.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / 'libondeviceinfer_wq.so'
+
+WQ_OK = 0
+WQ_ERR_INVALID_ARGUMENT = 1
+WQ_ERR_UNSUPPORTED = 2
+WQ_ERR_HIP = 3
+WQ_ERR_WORKSPACE = 4
+ABI_VERSION = 1
+
+W4_BLOCK_K = 128
+W4_META_BYTES = 40
+W8_BLOCK_K = 128
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_SIZE_P = ctypes.POINTER(ctypes.c_size_t)
+
+# name -> argtypes (restype is int for all but wq_last_error)
+_SIGNATURES = {
+    'wq_abi_version': [],
+    'wq_w4_repack_size': [_I64, _I64, _I64, _SIZE_P, _SIZE_P],
+    'wq_w4_repack': [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P],
+    'wq_w4_unpack': [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P],
+    'wq_w4_dequant': [_P, _P, _I64, _I64, _I64, _P, _P],
+    'wq_w4_decode': [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P],
+    'wq_w4a16_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
+    'wq_w4a16_linear': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, ctypes.c_size_t, _P],
+    'wq_w8_decode': [_P, _P, _I64, _I64, _P, _P],
+    'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P],
+    'wq_w8_quantize': [_P, _I64, _I64, _P, _P, _P, _P],
+}
+EXPORTED_SYMBOLS = ('wq_last_error', *_SIGNATURES)
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeLibraryError(RuntimeError):
+    """The HIP library is missing or unusable; there is no other code path."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library, with argtypes/restypes set."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise NativeLibraryError(
+                f'{LIB_PATH.name} is not built; run `python -m ondeviceinfer_amd.build` '
+                '(needs hipcc with gfx950 support)')
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.wq_last_error.restype = ctypes.c_char_p
+        lib.wq_last_error.argtypes = []
+        for name, args in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = args
+        version = lib.wq_abi_version()
+        if version != ABI_VERSION:
+            raise NativeLibraryError(f'ABI version {version} != expected {ABI_VERSION}; rebuild the library')
+        _lib = lib
+        return lib
+
+
+def _raise_for(status: int, what: str) -> None:
+    if status == WQ_OK:
+        return
+    msg = f'{what}: {load().wq_last_error().decode(errors="replace")}'
+    if status in (WQ_ERR_INVALID_ARGUMENT, WQ_ERR_UNSUPPORTED, WQ_ERR_WORKSPACE):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def _call(name: str, *args) -> None:
+    _raise_for(getattr(load(), name)(*args), name)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != 'cuda':
+            raise ValueError(f'expected a GPU tensor, got one on {t.device}; this build has no CPU path')
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f'tensors on different devices: {device} and {t.device}')
+    if device is None:
+        raise ValueError('no tensor given')
+    return device
+
+
+def _check(t: torch.Tensor, dtype: torch.dtype, shape: tuple, name: str) -> None:
+    if t.dtype != dtype:
+        raise TypeError(f'{name}: expected {dtype}, got {t.dtype}')
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f'{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}')
+    if not t.is_contiguous():
+        raise ValueError(f'{name}: must be contiguous')
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+# ----------------------------------------------------------------------------- W4
+
+def w4_repack_size(n: int, k: int, group_size: int) -> tuple[int, int]:
+    tb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    _call('wq_w4_repack_size', n, k, group_size, ctypes.byref(tb), ctypes.byref(mb))
+    return tb.value, mb.value
+
+
+def w4_repack(packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor | None,
+              n: int, k: int, group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """compressed-tensors tensors -> (tiles uint8, meta uint8) in the gfx950 layout."""
+    device = _require_gpu(packed, scale, zero)
+    _check(packed, torch.int32, (n, k // 8), 'weight_packed')
+    _check(scale, torch.float16, (n, k // group_size), 'weight_scale')
+    if zero is not None:
+        _check(zero, torch.int32, (n // 8, k // group_size), 'weight_zero_point')
+    tiles_bytes, meta_bytes = w4_repack_size(n, k, group_size)
+    tiles = torch.empty(tiles_bytes, dtype=torch.uint8, device=device)
+    meta = torch.empty(meta_bytes, dtype=torch.uint8, device=device)
+    _call('wq_w4_repack', _ptr(packed), _ptr(scale), _ptr(zero), n, k, group_size,
+          _ptr(tiles), _ptr(meta), _stream(device))
+    return tiles, meta
+
+
+def w4_unpack(tiles: torch.Tensor, meta: torch.Tensor, n: int, k: int,
+              group_size: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    device = _require_gpu(tiles, meta)
+    tb, mb = w4_repack_size(n, k, group_size)
+    _check(tiles, torch.uint8, (tb,), 'tiles')
+    _check(meta, torch.uint8, (mb,), 'meta')
+    packed = torch.empty((n, k // 8), dtype=torch.int32, device=device)
+    scale = torch.empty((n, k // group_size), dtype=torch.float16, device=device)
+    zero = torch.empty((n // 8, k // group_size), dtype=torch.int32, device=device)
+    _call('wq_w4_unpack', _ptr(tiles), _ptr(meta), n, k, group_size, _ptr(packed), _ptr(scale), _ptr(zero),
+          _stream(device))
+    return packed, scale, zero
+
+
+def w4_dequant(tiles: torch.Tensor, meta: torch.Tensor, n: int, k: int, group_size: int) -> torch.Tensor:
+    device = _require_gpu(tiles, meta)
+    tb, mb = w4_repack_size(n, k, group_size)
+    _check(tiles, torch.uint8, (tb,), 'tiles')
+    _check(meta, torch.uint8, (mb,), 'meta')
+    out = torch.empty((n, k), dtype=torch.float16, device=device)
+    _call('wq_w4_dequant', _ptr(tiles), _ptr(meta), n, k, group_size, _ptr(out), _stream(device))
+    return out
+
+
+def w4_decode(packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor | None,
+              g_idx: torch.Tensor | None, n: int, k: int, group_size: int) -> torch.Tensor:
+    """Explicit QDQ decode from compressed-tensors tensors (any group size, g_idx)."""
+    device = _require_gpu(packed, scale, zero, g_idx)
+    if packed.dtype != torch.int32 or packed.dim() != 2 or packed.shape[0] != n or packed.shape[1] * 8 < k:
+        raise ValueError(f'weight_packed must be int32 [{n}, {k // 8}], got {packed.dtype} {tuple(packed.shape)}')
+    if k % 8:
+        raise ValueError('decode needs k % 8 == 0')
+    packed = packed[:, :k // 8].contiguous()
+    scale32 = scale.float().contiguous()
+    if scale32.dim() != 2 or scale32.shape[0] != n:
+        raise ValueError(f'weight_scale must be [{n}, groups], got {tuple(scale.shape)}')
+    if zero is not None:
+        if zero.dtype != torch.int32 or tuple(zero.shape) != ((n + 7) // 8, scale32.shape[1]):
+            raise ValueError(f'weight_zero_point must be int32 [{(n + 7) // 8}, {scale32.shape[1]}]')
+        zero = zero.contiguous()
+    gi = None
+    if g_idx is not None and g_idx.numel():
+        gi = g_idx.to(torch.int32).contiguous()
+        if gi.numel() != k:
+            raise ValueError('weight_g_idx must have k entries')
+        if int(gi.min()) < 0 or int(gi.max()) >= scale32.shape[1]:
+            raise ValueError('weight_g_idx entries out of range')
+    out = torch.empty((n, k), dtype=torch.float16, device=device)
+    _call('wq_w4_decode', _ptr(packed), _ptr(scale32), _ptr(zero), _ptr(gi), n, k, scale32.shape[1], group_size,
+          _ptr(out), _stream(device))
+    return out
+
+
+def w4a16_workspace_size(m: int, n: int, k: int, group_size: int) -> int:
+    b = ctypes.c_size_t()
+    _call('wq_w4a16_workspace_size', m, n, k, group_size, ctypes.byref(b))
+    return b.value
+
+
+def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: int, group_size: int,
+                 out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``y[m, n] = x[m, k] . dequant(W)^T`` on the repacked weight."""
+    device = _require_gpu(x, tiles, meta, out)
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise TypeError(f'x must be a 2-D float16 tensor, got {x.dtype} {tuple(x.shape)}')
+    m, k = x.shape
+    x = _aligned(x.contiguous())
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float16, device=device)
+    else:
+        _check(out, torch.float16, (m, n), 'out')
+        if out.data_ptr() % 16:
+            raise ValueError('out must be 16-byte aligned')
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    _call('wq_w4a16_linear', _ptr(x), m, k, _ptr(tiles), _ptr(meta), n, group_size, _ptr(out), ws_ptr, ws_bytes,
+          _stream(device))
+    return out
+
+
+# ----------------------------------------------------------------------------- W8
+
+def w8_decode(qweight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    device = _require_gpu(qweight, scale)
+    if qweight.dtype != torch.int8 or qweight.dim() != 2:
+        raise TypeError(f'expected a 2-D INT8 weight, got {qweight.dtype} {tuple(qweight.shape)}')
+    n, k = qweight.shape
+    s = scale.float().reshape(-1).contiguous()
+    if s.numel() != n:
+        raise ValueError(f'scale must have {n} entries, got {s.numel()}')
+    out = torch.empty((n, k), dtype=torch.float16, device=device)
+    _call('wq_w8_decode', _ptr(qweight.contiguous()), _ptr(s), n, k, _ptr(out), _stream(device))
+    return out
+
+
+def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """``y = x . (q * scale)^T (+ bias)`` straight from the row-major INT8 weight."""
+    device = _require_gpu(x, qweight, scale, bias, out)
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise TypeError(f'x must be a 2-D float16 tensor, got {x.dtype} {tuple(x.shape)}')
+    if qweight.dtype != torch.int8 or qweight.dim() != 2:
+        raise TypeError(f'qweight must be a 2-D INT8 tensor, got {qweight.dtype}')
+    n, k = qweight.shape
+    if x.shape[1] != k:
+        raise ValueError(f'input has {x.shape[1]} features, expected {k}')
+    if scale.dtype != torch.float16 or scale.numel() != n:
+        raise ValueError(f'scale must be float16 with {n} entries')
+    if bias is not None and (bias.dtype != torch.float16 or bias.numel() != n):
+        raise ValueError('bias must be FP16 with one entry per output feature')
+    m = x.shape[0]
+    x = _aligned(x.contiguous())
+    q = _aligned(qweight.contiguous())
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float16, device=device)
+    else:
+        _check(out, torch.float16, (m, n), 'out')
+    _call('wq_w8a16_linear', _ptr(x), m, k, _ptr(q), _ptr(scale.contiguous()), n,
+          _ptr(None if bias is None else bias.contiguous()), _ptr(out), _stream(device))
+    return out
+
+
+def w8_quantize(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row symmetric INT8 quantization on the GPU -> (qweight int8, scale fp16)."""
+    device = _require_gpu(weight)
+    n, k = weight.shape
+    w32 = weight.to(torch.float32).contiguous()
+    q = torch.empty((n, k), dtype=torch.int8, device=device)
+    s = torch.empty(n, dtype=torch.float16, device=device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    _call('wq_w8_quantize', _ptr(w32), n, k, _ptr(q), _ptr(s), _ptr(flags), _stream(device))
+    f = int(flags.item())
+    if f & 1:
+        raise ValueError('linear weight contains NaN or infinity')
+    if f & 2:
+        raise OverflowError('row scale is not representable in scale_dtype')
+    return q, s

@@ -1,0 +1,96 @@
+// C-ABI entry points for the linear kernels, plus the error channel.
+#include "wq_common.h"
+#include "wq_status.h"
+
+namespace wq {
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
+                     half_t* y, hipStream_t s);
+int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
+                     half_t* y, hipStream_t s);
+int launch_w8_generic(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
+                      half_t* y, hipStream_t s);
+int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
+                   hipStream_t s);
+int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
+                   half_t* y, hipStream_t s);
+
+// Largest M served by the MFMA GEMV (4 chunks of 16 activation rows).
+constexpr int64_t kSkinnyMaxM = 64;
+
+namespace {
+
+int linear_shape_check(int64_t m, int64_t n, int64_t k) {
+  WQ_REQUIRE(m >= 0 && n > 0 && k > 0, WQ_ERR_INVALID_ARGUMENT, "bad linear shape m=%lld n=%lld k=%lld",
+             (long long)m, (long long)n, (long long)k);
+  WQ_REQUIRE(m <= 0x7FFFFFFF && n <= 0x7FFFFFFF && k <= 0x7FFFFFFF && m * k < (1LL << 40), WQ_ERR_UNSUPPORTED,
+             "linear shape too large m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  return WQ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace wq
+
+using namespace wq;
+
+extern "C" const char* wq_last_error(void) { return g_last_error; }
+
+extern "C" int wq_abi_version(void) { return WQ_ABI_VERSION; }
+
+extern "C" int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t group_size, size_t* bytes) {
+  if (int st = linear_shape_check(m, n, k)) return st;
+  WQ_REQUIRE(bytes, WQ_ERR_INVALID_ARGUMENT, "null size output");
+  (void)group_size;
+  *bytes = 0;  // every current kernel reduces inside its workgroup
+  return WQ_OK;
+}
+
+extern "C" int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, const void* meta,
+                               int64_t n, int64_t group_size, uint16_t* y, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (int st = linear_shape_check(m, n, k)) return st;
+  WQ_REQUIRE(n % 8 == 0 && group_size % kW4BlockK == 0 && group_size > 0 && k % group_size == 0,
+             WQ_ERR_UNSUPPORTED, "W4A16 needs n %% 8 == 0, group_size %% 128 == 0, k %% group_size == 0 "
+             "(n=%lld k=%lld group=%lld)", (long long)n, (long long)k, (long long)group_size);
+  WQ_REQUIRE(x && tiles && meta && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(aligned16(x) && aligned16(tiles) && aligned16(y) && (reinterpret_cast<uintptr_t>(meta) & 7u) == 0,
+             WQ_ERR_INVALID_ARGUMENT, "x, tiles and y must be 16-byte aligned and meta 8-byte aligned");
+  if (m == 0) return WQ_OK;
+  const half_t* xh = reinterpret_cast<const half_t*>(x);
+  half_t* yh = reinterpret_cast<half_t*>(y);
+  if (m <= kSkinnyMaxM)
+    return launch_w4_skinny(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
+                            reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
+  return launch_w4_gemm(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
+                        reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
+}
+
+extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight, const uint16_t* scale,
+                               int64_t n, const uint16_t* bias, uint16_t* y, void* stream) {
+  if (int st = linear_shape_check(m, n, k)) return st;
+  WQ_REQUIRE(x && qweight && scale && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (m == 0) return WQ_OK;
+  const half_t* xh = reinterpret_cast<const half_t*>(x);
+  const half_t* sh = reinterpret_cast<const half_t*>(scale);
+  const half_t* bh = reinterpret_cast<const half_t*>(bias);
+  half_t* yh = reinterpret_cast<half_t*>(y);
+  if (k % kW8BlockK != 0 || !aligned16(x) || !aligned16(qweight))
+    return launch_w8_generic(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
+  if (m <= kSkinnyMaxM) return launch_w8_skinny(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
+  return launch_w8_gemm(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
+}

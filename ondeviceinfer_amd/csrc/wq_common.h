@@ -1,0 +1,101 @@
+// Shared device helpers for the gfx950 weight-only quantized Linear.
+//
+// Conventions used by every kernel in this directory:
+//  * fp16 tensors cross the C ABI as uint16_t bit patterns; inside kernels
+//    they are _Float16 vectors.
+//  * MFMA v_mfma_f32_16x16x32_f16 is used with the *weights* as the A operand
+//    (16 output rows n) and the activations as the B operand (16 columns m),
+//    so the accumulator lane l holds D[n = 4*(l/16) + v][m = l%16], v = 0..3.
+//    Lane l supplies A row l%16 and B column l%16, each with 8 consecutive k
+//    taken from k-slot l/16; A and B use the same (lane, register) -> k map,
+//    which is all the dot product needs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace wq {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kW4BlockK = 128;     // k extent of one W4 tile block (one 1 KiB wave load)
+constexpr int kW4MetaBytes = 40;   // per (16-row tile, group): 16 fp16 scales + 2 zero words
+constexpr int kW8BlockK = 128;     // k extent of one INT8 wave block (2 x 16 B per lane)
+
+__device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ __forceinline__ uint32_t as_u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Zero-point constants for one row: c_lo = -(1024 + z), c_hi = -(64 + z) as
+// fp16 pairs.  -(1024+z) has exponent 25 and mantissa z; -(64+z) has exponent
+// 21 and mantissa 16*z.
+__device__ __forceinline__ void w4_zero_consts(uint32_t z, uint32_t& c_lo, uint32_t& c_hi) {
+  const uint32_t zz = z * 0x00010001u;
+  c_lo = zz | 0xE400E400u;
+  c_hi = (zz << 4) | 0xD400D400u;
+}
+
+// One tile word (nibble p holds element {0,2,4,6,1,3,5,7}[p]) -> the eight
+// exact fp16 values (q_e - z), e = 0..7 in order.  OR-ing a nibble into the
+// mantissa of 1024.0 gives 1024+q exactly; the high nibble of each byte lands
+// as 1024+16q and is brought back with an exact fma by 1/16.
+__device__ __forceinline__ half8_t w4_word_to_h8(uint32_t w, uint32_t c_lo, uint32_t c_hi) {
+  const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
+  const uint32_t w8 = w >> 8;
+  const half2_t t0 = as_h2((w & 0x000F000Fu) | 0x64006400u);
+  const half2_t t1 = as_h2((w & 0x00F000F0u) | 0x64006400u);
+  const half2_t t2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u);
+  const half2_t t3 = as_h2((w8 & 0x00F000F0u) | 0x64006400u);
+  const half2_t p0 = t0 + as_h2(c_lo);
+  const half2_t p1 = __builtin_elementwise_fma(t1, sixteenth, as_h2(c_hi));
+  const half2_t p2 = t2 + as_h2(c_lo);
+  const half2_t p3 = __builtin_elementwise_fma(t3, sixteenth, as_h2(c_hi));
+  half8_t r;
+  r.s01 = p0; r.s23 = p1; r.s45 = p2; r.s67 = p3;
+  return r;
+}
+
+// Same, multiplied by the group scale: fp16((q - z) * s), which is the
+// reference decode bit for bit ((q - z) is exact, the product rounds once).
+__device__ __forceinline__ half8_t w4_word_to_h8_scaled(uint32_t w, uint32_t c_lo, uint32_t c_hi, half2_t s2) {
+  half8_t v = w4_word_to_h8(w, c_lo, c_hi);
+  half8_t s8;
+  s8.s01 = s2; s8.s23 = s2; s8.s45 = s2; s8.s67 = s2;
+  return v * s8;
+}
+
+// Four signed int8 (natural order) -> four exact fp16.  Flipping the sign bit
+// gives q+128 as an unsigned byte; placing it under the exponent byte 0x64
+// yields 1024+128+q, and subtracting 1152 leaves q.
+__device__ __forceinline__ half4_t i8x4_to_h4(uint32_t w) {
+  const uint32_t u = w ^ 0x80808080u;
+  const half2_t bias = as_h2(0xE480E480u);  // -1152
+  const half2_t lo = as_h2(__builtin_amdgcn_perm(u, 0x64646464u, 0x00050004u)) + bias;
+  const half2_t hi = as_h2(__builtin_amdgcn_perm(u, 0x64646464u, 0x00070006u)) + bias;
+  half4_t r;
+  r.s01 = lo; r.s23 = hi;
+  return r;
+}
+
+__device__ __forceinline__ half8_t i8x8_to_h8(uint32_t w0, uint32_t w1) {
+  half8_t r;
+  r.s0123 = i8x4_to_h4(w0);
+  r.s4567 = i8x4_to_h4(w1);
+  return r;
+}
+
+__device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half8_t ld_h8(const half_t* p) {
+  return *reinterpret_cast<const half8_t*>(p);
+}
+
+}  // namespace wq

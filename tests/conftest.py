@@ -1,0 +1,23 @@
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line('markers', 'gpu: needs an MI355X (gfx950) GPU; run with -m gpu')
+
+
+@pytest.fixture(scope='session')
+def gpu():
+    """The GPU device; GPU tests fail loudly when the HIP library is missing."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip('no GPU visible')
+    from ondeviceinfer_amd import _native
+    _native.load()
+    return torch.device('cuda:0')

@@ -1,0 +1,57 @@
+"""The C-ABI library loads, exports every symbol the header declares, and
+rejects malformed requests before any GPU work (CPU-only checks)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from ondeviceinfer_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / 'include' / 'ondeviceinfer_wq.h'
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r'/\*.*?\*/', '', HEADER.read_text(), flags=re.S)
+    return re.findall(r'^\s*(?:const\s+char\s*\*|int)\s+(wq_\w+)\s*\(', text, flags=re.M)
+
+
+def test_header_declares_the_bound_entry_points():
+    names = declared_functions()
+    assert len(names) == len(set(names)) >= 12
+    assert set(names) == set(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.wq_abi_version() == _native.ABI_VERSION
+
+
+def _status(fn, *args):
+    return getattr(_native.load(), fn)(*args)
+
+
+def test_shape_validation_happens_on_the_host():
+    tb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    assert _status('wq_w4_repack_size', 5120, 5120, 128, ctypes.byref(tb), ctypes.byref(mb)) == _native.WQ_OK
+    assert tb.value == 5120 * 5120 // 2 and mb.value == 320 * 40 * 40
+    assert _status('wq_w4_repack_size', 12, 5120, 128, ctypes.byref(tb), ctypes.byref(mb)) == _native.WQ_ERR_UNSUPPORTED
+    assert b'n % 8' in _native.load().wq_last_error()
+    assert _status('wq_w4_repack_size', 16, 5120, 64, ctypes.byref(tb), ctypes.byref(mb)) == _native.WQ_ERR_UNSUPPORTED
+    assert _status('wq_w4_repack_size', 0, 5120, 128, ctypes.byref(tb), ctypes.byref(mb)) == \
+        _native.WQ_ERR_INVALID_ARGUMENT
+    # k not a multiple of the group -> rejected before any launch
+    assert _status('wq_w4a16_linear', 1, 1, 200, 1, 1, 16, 128, 1, None, 0, None) == _native.WQ_ERR_UNSUPPORTED
+    # null pointers -> rejected
+    assert _status('wq_w4a16_linear', None, 1, 256, None, None, 16, 128, None, None, 0, None) == \
+        _native.WQ_ERR_INVALID_ARGUMENT
+    assert _status('wq_w8_quantize', None, 0, 4, None, None, None, None) == _native.WQ_ERR_INVALID_ARGUMENT
+
+
+def test_status_maps_to_python_exceptions():
+    with pytest.raises(ValueError, match='n % 8'):
+        _native.w4_repack_size(12, 256, 128)
+    assert _native.w4_repack_size(16, 256, 128) == (16 * 128, 2 * 40)
+    assert _native.w4a16_workspace_size(1, 5120, 5120, 128) == 0

@@ -1,0 +1,282 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Bars: repack/unpack/decode/quantize bit-exact; linear outputs within
+max|d| <= 1e-2 * ||y_ref||_inf, mean|d|/mean|y_ref| <= 2e-3 (fp32
+accumulation), cosine >= 0.9999 and rel-L2 <= 0.02 (``oracle.qdq.parity_ok``).
+Full BASELINE shapes are checked whole at M=1 and on sampled activation rows
+at M=4096 (the oracle restricted to those rows is the same computation).
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import qdq, synth, tile_layout
+from ondeviceinfer_amd import _native
+from ondeviceinfer_amd import quantization as q8
+from ondeviceinfer_amd.quantized_model import int8_weight_only_linear
+from ondeviceinfer_amd.weight_quantization import backend as wq
+
+pytestmark = pytest.mark.gpu
+KAT = json.loads((Path(__file__).parent / 'golden' / 'weight_quant_kat.json').read_text())
+
+
+def dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint16)
+
+
+def check_parity(actual, expected, label):
+    m = qdq.parity_metrics(actual, expected)
+    print(label, {k: (round(v, 8) if isinstance(v, float) else v) for k, v in m.items()}, flush=True)
+    assert qdq.parity_ok(m), (label, m)
+
+
+def prepared_w4(weights, name, device, group_size=128):
+    layer = {k: dev(v, device) for k, v in weights.items()}
+    backend = wq.CompressedLinearBackend('marlin', group_size=group_size)
+    backend.prepare(layer, name)
+    return backend, layer
+
+
+# ------------------------------------------------------------------ layout / decode, bit-exact
+
+@pytest.mark.parametrize('n,k,g,sym', [(16, 256, 128, False), (1000, 1024, 128, False), (24, 512, 256, True),
+                                       (5120, 5120, 128, False)])
+def test_repack_is_the_tile_layout_and_round_trips(gpu, n, k, g, sym):
+    weights, _ = synth.w4_case(n, k, 1, seed=n, group_size=g, symmetric=sym, name='p.weight')
+    packed, scale, zero = weights['p.weight_packed'], weights['p.weight_scale'], weights.get('p.weight_zero_point')
+    tiles, meta = _native.w4_repack(dev(packed, gpu), dev(scale, gpu), None if zero is None else dev(zero, gpu),
+                                    n, k, g)
+    ref_tiles, ref_meta = tile_layout.w4_repack(packed, scale, zero, n, k, g)
+    assert np.array_equal(host(tiles), ref_tiles.view(np.uint8).ravel())
+    assert np.array_equal(host(meta), ref_meta.ravel())
+    p2, s2, z2 = _native.w4_unpack(tiles, meta, n, k, g)
+    assert np.array_equal(host(p2), packed)
+    assert np.array_equal(bits(host(s2)), bits(scale))
+    if zero is None:
+        assert np.all(host(z2).view(np.uint32) == tile_layout.SYMMETRIC_ZERO_WORD)
+    else:
+        assert np.array_equal(host(z2), zero)
+    # the kernels' own unpack arithmetic reproduces the reference decode bit for bit
+    deq = _native.w4_dequant(tiles, meta, n, k, g)
+    assert np.array_equal(bits(host(deq)), bits(qdq.decode_weight(weights, 'p.weight', group_size=g)))
+
+
+def test_decode_known_answers_on_gpu(gpu):
+    c = KAT['kat_group_decode']
+    w = {'mlp.up_proj.weight_packed': torch.tensor(c['weight_packed'], dtype=torch.int32, device=gpu),
+         'mlp.up_proj.weight_shape': torch.tensor(c['weight_shape']),
+         'mlp.up_proj.weight_scale': torch.tensor(c['weight_scale'], device=gpu),
+         'mlp.up_proj.weight_zero_point': torch.tensor(c['weight_zero_point'], dtype=torch.int32, device=gpu)}
+    assert host(wq.decode_weight(w, c['name'], group_size=c['group_size'])).tolist() == c['expected']
+    c = KAT['kat_symmetric']
+    w = {'self_attn.q_proj.weight_packed': torch.tensor(c['weight_packed'], dtype=torch.int32, device=gpu),
+         'self_attn.q_proj.weight_shape': torch.tensor(c['weight_shape']),
+         'self_attn.q_proj.weight_scale': torch.tensor(c['weight_scale'], device=gpu)}
+    assert host(wq.decode_weight(w, c['name'], group_size=c['group_size'])).tolist() == c['expected']
+    c = KAT['kat_int8_channel']
+    w = {c['name']: torch.tensor(c['weight'], dtype=torch.int8, device=gpu),
+         'self_attn.q_proj.weight_scale': torch.tensor(c['weight_scale'], device=gpu)}
+    assert host(wq.decode_weight(w, c['name'])).tolist() == c['expected']
+
+
+@pytest.mark.parametrize('use_gidx', [False, True])
+@pytest.mark.parametrize('sym', [False, True])
+def test_decode_random_bit_exact(gpu, use_gidx, sym):
+    n, k, g = 64, 1024, 128
+    weights, _ = synth.w4_case(n, k, 1, seed=5, group_size=g, symmetric=sym, name='p.weight')
+    if use_gidx:
+        weights['p.weight_g_idx'] = np.random.default_rng(1).permutation(np.arange(k) // g).astype(np.int32)
+    got = wq.decode_weight({kk: dev(v, gpu) for kk, v in weights.items()}, 'p.weight', group_size=g)
+    assert np.array_equal(bits(host(got)), bits(qdq.decode_weight(weights, 'p.weight', group_size=g)))
+
+
+# ------------------------------------------------------------------ W4A16 linear
+
+@pytest.mark.parametrize('m', [1, 2, 15, 16, 17, 33, 64, 65, 128, 300])
+@pytest.mark.parametrize('n,k', [(16, 128), (1000, 1024), (1024, 5120)])
+def test_w4a16_linear_parity_small(gpu, m, n, k):
+    name = 'mlp.up_proj.weight'
+    weights, x = synth.w4_case(n, k, m, seed=m * 7 + n, name=name)
+    backend, layer = prepared_w4(weights, name, gpu)
+    y = backend.linear(dev(x, gpu), layer, name)
+    check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 m={m} n={n} k={k}')
+
+
+def test_w4a16_group_256_and_symmetric(gpu):
+    for g, sym in ((256, False), (128, True)):
+        weights, x = synth.w4_case(256, 2048, 3, seed=g, group_size=g, symmetric=sym, name='p.weight')
+        backend, layer = prepared_w4(weights, 'p.weight', gpu, group_size=g)
+        y = backend.linear(dev(x, gpu), layer, 'p.weight')
+        check_parity(host(y), qdq.qdq_linear(x, weights, 'p.weight', group_size=g), f'w4 g={g} sym={sym}')
+
+
+@pytest.mark.parametrize('k,n', [(5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120), (5120, 7168),
+                                 (5120, 34816)])
+def test_w4a16_decode_full_shapes(gpu, k, n):
+    """configs 2 and 4: the Qwen3-14B projection shapes at M=1, whole output."""
+    name = 'mlp.up_proj.weight'
+    weights, x = synth.w4_case(n, k, 1, seed=0, name=name)
+    backend, layer = prepared_w4(weights, name, gpu)
+    y = backend.linear(dev(x, gpu), layer, name)
+    check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 decode {k}->{n}')
+
+
+@pytest.mark.parametrize('k,n', [(5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120)])
+def test_w4a16_prefill_full_shapes_sampled_rows(gpu, k, n):
+    """config 3: M=4096 on the full weight; 48 activation rows checked whole."""
+    name = 'mlp.up_proj.weight'
+    weights, _ = synth.w4_case(n, k, 1, seed=1, name=name)
+    x = np.random.default_rng(2).standard_normal((4096, k), dtype=np.float32).astype(np.float16)
+    backend, layer = prepared_w4(weights, name, gpu)
+    y = host(backend.linear(dev(x, gpu), layer, name))
+    rows = np.random.default_rng(3).choice(4096, size=48, replace=False)
+    rows.sort()
+    check_parity(y[rows], qdq.qdq_linear(x[rows], weights, name), f'w4 prefill {k}->{n} rows')
+    assert np.isfinite(y).all()
+
+
+def test_w4a16_lm_head_sampled_columns(gpu):
+    """config 4's lm_head 5120->151936 at M in {1, 32}: 4096 output columns checked."""
+    name = 'lm_head.weight'
+    weights, x = synth.w4_case(151936, 5120, 32, seed=9, name=name)
+    backend, layer = prepared_w4(weights, name, gpu)
+    cols = np.sort(np.random.default_rng(4).choice(151936, size=4096, replace=False))
+    w_cols = qdq.decode_rows(weights, name, cols)
+    for m in (1, 32):
+        y = host(backend.linear(dev(x[:m], gpu), layer, name))
+        check_parity(y[:, cols], qdq.linear_fp32(x[:m], w_cols), f'w4 lm_head m={m}')
+
+
+def test_w4a16_repeat_calls_are_bitwise_identical(gpu):
+    name = 'mlp.down_proj.weight'
+    weights, x = synth.w4_case(5120, 17408, 4, seed=3, name=name)
+    backend, layer = prepared_w4(weights, name, gpu)
+    for m in (1, 4):
+        xd = dev(x[:m], gpu)
+        first = backend.linear(xd, layer, name).clone()
+        for _ in range(5):
+            assert torch.equal(backend.linear(xd, layer, name), first)
+
+
+def test_backend_shapes_counters_and_row_split(gpu, monkeypatch):
+    name = 'self_attn.o_proj.weight'
+    weights, x = synth.w4_case(512, 1024, 24, seed=8, name=name)
+    backend, layer = prepared_w4(weights, name, gpu)
+    assert 'self_attn.o_proj.weight_packed' not in layer and 'self_attn.o_proj._prepared' in layer
+    x3 = dev(x.reshape(2, 12, 1024), gpu)
+    y = backend.linear(x3, layer, name)
+    assert y.shape == (2, 12, 512) and backend.calls == 1 and backend.gemm_calls == 1
+    backend.marlin_max_rows_per_call = 16
+    y2 = backend.linear(x3, layer, name)
+    assert backend.gemm_calls == 3 and backend.fallback_count == 0
+    check_parity(host(y2).reshape(24, 512), qdq.qdq_linear(x, weights, name), 'row split')
+    assert backend.linear(dev(x[:0], gpu), layer, name).shape == (0, 512)
+
+
+def test_reference_int4_backend_matches_oracle(gpu):
+    name = 'mlp.gate_proj.weight'
+    weights, x = synth.w4_case(256, 1024, 5, seed=2, name=name)
+    layer = {k: dev(v, gpu) for k, v in weights.items()}
+    ref = wq.CompressedLinearBackend('reference_int4')
+    y = ref.linear(dev(x, gpu), layer, name)
+    assert ref.explicit_dequant_bytes == 256 * 1024 * 2
+    check_parity(host(y), qdq.qdq_linear(x, weights, name), 'reference_int4')
+
+
+def test_w4a16_rejects_unsupported_shapes(gpu):
+    weights, _ = synth.w4_case(16, 256, 1, name='p.weight')
+    layer = {k: dev(v, gpu) for k, v in weights.items()}
+    with pytest.raises(ValueError):
+        wq.CompressedLinearBackend('marlin', group_size=64).prepare(layer, 'p.weight')
+    layer['p.weight_g_idx'] = torch.zeros(256, dtype=torch.int32, device=gpu)
+    with pytest.raises(ValueError, match='G-index'):
+        wq.CompressedLinearBackend('marlin').prepare(layer, 'p.weight')
+
+
+# ------------------------------------------------------------------ INT8 (W8A16)
+
+def int8_ref(x, q, s, bias=None):
+    return qdq.linear_fp32(x, qdq.dequantize_linear_weight(q, s), bias)
+
+
+@pytest.mark.parametrize('m', [1, 3, 16, 40, 64, 65, 200])
+@pytest.mark.parametrize('n,k', [(40, 256), (1000, 1024), (5120, 5120)])
+def test_w8a16_linear_parity(gpu, m, n, k):
+    _, q, s, x = synth.int8_case(n, k, m, seed=m + n)
+    y = _native.w8a16_linear(dev(x, gpu), dev(q, gpu), dev(s, gpu))
+    check_parity(host(y), int8_ref(x, q, s), f'w8 m={m} n={n} k={k}')
+
+
+def test_w8a16_config1_and_bias_and_generic_shapes(gpu):
+    w, q, s, x = synth.int8_case(5120, 5120, 1, seed=0)          # config 1
+    y = _native.w8a16_linear(dev(x, gpu), dev(q, gpu), dev(s, gpu))
+    check_parity(host(y), int8_ref(x, q, s), 'w8 config1')
+    rng = np.random.default_rng(19)
+    for m, n, k in ((6, 11, 13), (2, 33, 200), (300, 24, 96)):    # k % 128 != 0 -> one-wave-per-output kernel
+        _, q, s, x = synth.int8_case(n, k, m, seed=n)
+        b = rng.standard_normal(n).astype(np.float16)
+        y = _native.w8a16_linear(dev(x, gpu), dev(q, gpu), dev(s, gpu), bias=dev(b, gpu))
+        check_parity(host(y), int8_ref(x, q, s, b), f'w8 generic m={m} n={n} k={k}')
+
+
+def test_int8_quantizer_bit_exact(gpu):
+    for case in ('kat_int8_zero_tiny_rows', 'kat_int8_half_even', 'kat_int8_stored_scale', 'kat_int8_clamp'):
+        c = KAT[case]
+        got = q8.quantize_linear_weight(torch.tensor(c['weight'], device=gpu))
+        assert host(got.qweight).tolist() == c['expected_q'], case
+        assert host(got.scale).view(np.uint16).tolist() == c['expected_scale_f16_bits'], case
+    w = (np.random.default_rng(0).standard_normal((5120, 5120), dtype=np.float32) * np.float32(0.02)).astype(np.float16)
+    got = q8.quantize_linear_weight(dev(w, gpu))
+    qr, sr = qdq.quantize_linear_weight(w)
+    assert np.array_equal(host(got.qweight), qr)
+    assert np.array_equal(bits(host(got.scale)), bits(sr))
+    with pytest.raises(ValueError, match='NaN'):
+        q8.quantize_linear_weight(torch.tensor([[1.0, float('nan')]], device=gpu))
+    with pytest.raises(OverflowError):
+        q8.quantize_linear_weight(torch.tensor([[1e7 * 127, 1.0]], device=gpu))
+
+
+def test_int8_modules_match_reference_semantics(gpu):
+    torch.manual_seed(19)
+    weight = torch.randn(11, 13, device=gpu) * 0.2
+    qw = q8.quantize_linear_weight(weight)
+    x = torch.randn(2, 3, 13, device=gpu, dtype=torch.float16)
+    bias = torch.randn(11, device=gpu, dtype=torch.float16)
+    scratch = q8.FP16DequantScratch.allocate(weight.numel(), device=gpu)
+    deq = qw.dequantize(scratch).clone()
+    assert deq.data_ptr() != scratch.buffer.data_ptr()
+    assert qw.dequantize(scratch).data_ptr() == scratch.buffer.data_ptr()
+    assert np.array_equal(bits(host(deq)), bits(qdq.dequantize_linear_weight(host(qw.qweight), host(qw.scale))))
+    actual = q8.quantized_linear(x, qw, scratch, bias=bias)
+    expected = qdq.linear_fp32(host(x), host(deq), host(bias))
+    check_parity(host(actual), expected, 'quantized_linear')
+    assert torch.allclose(actual, torch.nn.functional.linear(x, weight.half(), bias), atol=2e-2, rtol=2e-2)
+    # the INT8 v1 runtime linear (quantized_model.py:76-121)
+    _, q, s, xx = synth.int8_case(1024, 5120, 1, seed=4)
+    weights = {'mlp.down_proj.qweight': dev(q, gpu), 'mlp.down_proj.scale': dev(s, gpu)}
+    y = int8_weight_only_linear(dev(xx.reshape(1, 1, 5120), gpu), weights, 'mlp.down_proj.weight',
+                                torch.empty(1024 * 5120, dtype=torch.float16, device=gpu))
+    assert y.shape == (1, 1, 1024)
+    check_parity(host(y).reshape(1, 1024), int8_ref(xx, q, s), 'int8_weight_only_linear')
+
+
+def test_w8a16_backend(gpu):
+    name = 'mlp.up_proj.weight'
+    _, q, s, x = synth.int8_case(256, 1024, 7, seed=6)
+    layer = {name: dev(q, gpu), 'mlp.up_proj.weight_scale': dev(s.reshape(-1, 1), gpu)}
+    backend = wq.CompressedLinearBackend('w8a16')
+    backend.prepare(layer, name)
+    y = backend.linear(dev(x, gpu), layer, name)
+    check_parity(host(y), int8_ref(x, q, s), 'w8a16 backend')

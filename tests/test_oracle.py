@@ -1,0 +1,246 @@
+"""Pins the CPU oracle (``oracle/``) before anything is compared against it.
+
+Each check is independent of the oracle's own formulas: the reference's
+known-answer vectors (``tests/golden/weight_quant_kat.json``), scalar
+brute-force re-derivations with Python ints/floats and ``struct`` fp16
+rounding, hand-derived INT8 vectors, and the reference's quantizer invariants.
+"""
+import json
+import math
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import qdq, synth, tile_layout
+
+KAT = json.loads((Path(__file__).parent / 'golden' / 'weight_quant_kat.json').read_text())
+
+
+def f16(value: float) -> np.float16:
+    """Round a Python float to fp16 (IEEE round-to-nearest-even via struct)."""
+    return np.frombuffer(struct.pack('<e', value), dtype=np.float16)[0]
+
+
+# --------------------------------------------------------------------------- unpack / pack
+
+def test_unpack_kat_both_axes():
+    c = KAT['kat_unpack']
+    packed = np.array(c['packed'], dtype=np.int32)
+    assert qdq.unpack_unsigned(packed, 4, 1, 8).tolist() == c['expected_axis1']
+    assert qdq.unpack_unsigned(packed, 4, 0, 8).tolist() == c['expected_axis0']
+
+
+def test_unpack_matches_unsigned_scalar_extraction():
+    rng = np.random.default_rng(1)
+    words = rng.integers(0, 2**32, size=(5, 3), dtype=np.uint64)
+    packed = words.astype(np.uint32).view(np.int32)
+    got = qdq.unpack_unsigned(packed, 4, 1, 24)
+    for r in range(5):
+        for c in range(24):
+            assert got[r, c] == (int(words[r, c // 8]) >> (4 * (c % 8))) & 0xF
+    got0 = qdq.unpack_unsigned(packed, 4, 0, 40)
+    for r in range(40):
+        for c in range(3):
+            assert got0[r, c] == (int(words[r // 8, c]) >> (4 * (r % 8))) & 0xF
+
+
+def test_pack_is_inverse_and_reproduces_kat_words():
+    assert qdq.pack_unsigned(np.arange(8).reshape(1, 8), 4, 1).tolist() == KAT['kat_unpack']['packed']
+    # zero points of rows (0, 1) for groups (0, 1) are (0, 1) and (2, 3): words 0x10, 0x32
+    assert qdq.pack_unsigned(np.array([[0, 2], [1, 3]]), 4, 0).tolist() == KAT['kat_group_decode']['weight_zero_point']
+    rng = np.random.default_rng(2)
+    codes = rng.integers(0, 16, size=(16, 64))
+    assert np.array_equal(qdq.unpack_unsigned(qdq.pack_unsigned(codes, 4, 1), 4, 1, 64), codes)
+    assert np.array_equal(qdq.unpack_unsigned(qdq.pack_unsigned(codes, 4, 0), 4, 0, 16), codes)
+
+
+# --------------------------------------------------------------------------- decode
+
+def _kat_weights(c, prefix):
+    w = {f'{prefix}.weight_packed': np.array(c['weight_packed'], dtype=np.int32),
+         f'{prefix}.weight_shape': np.array(c['weight_shape']),
+         f'{prefix}.weight_scale': np.array(c['weight_scale'], dtype=np.float32)}
+    if 'weight_zero_point' in c:
+        w[f'{prefix}.weight_zero_point'] = np.array(c['weight_zero_point'], dtype=np.int32)
+    return w
+
+
+def test_group_zero_point_and_scale_kat():
+    c = KAT['kat_group_decode']
+    got = qdq.decode_weight(_kat_weights(c, 'mlp.up_proj'), c['name'], group_size=c['group_size'])
+    assert got.dtype == np.float16 and got.tolist() == c['expected']
+
+
+def test_symmetric_bias_kat():
+    c = KAT['kat_symmetric']
+    got = qdq.decode_weight(_kat_weights(c, 'self_attn.q_proj'), c['name'], group_size=c['group_size'])
+    assert got.tolist() == c['expected']
+
+
+def test_int8_channel_kat():
+    c = KAT['kat_int8_channel']
+    w = {c['name']: np.array(c['weight'], dtype=np.int8),
+         'self_attn.q_proj.weight_scale': np.array(c['weight_scale'], dtype=np.float32)}
+    assert qdq.decode_weight(w, c['name']).tolist() == c['expected']
+    q, s = w[c['name']], w['self_attn.q_proj.weight_scale'].reshape(-1)
+    assert qdq.dequantize_linear_weight(q, s).tolist() == c['expected']
+
+
+def test_sampled_rows_kat():
+    c = KAT['kat_sampled_rows']
+    scale = np.array(c['weight_scale_f16_bits'], dtype=np.uint16).view(np.float16)
+    w = {'mlp.up_proj.weight_packed': np.full(c['packed_shape'], c['packed_word'], dtype=np.int32),
+         'mlp.up_proj.weight_shape': np.array(c['weight_shape']),
+         'mlp.up_proj.weight_scale': scale,
+         'mlp.up_proj.weight_zero_point': np.array(c['weight_zero_point'], dtype=np.int32)}
+    rows = np.array(c['rows'])
+    assert np.array_equal(qdq.decode_rows(w, c['name'], rows), qdq.decode_weight(w, c['name'])[rows])
+
+
+@pytest.mark.parametrize('use_gidx', [False, True])
+@pytest.mark.parametrize('symmetric', [False, True])
+def test_decode_matches_scalar_brute_force(use_gidx, symmetric):
+    rng = np.random.default_rng(3)
+    n, k, g = 16, 256, 64
+    codes = rng.integers(0, 16, size=(n, k))
+    zeros = rng.integers(0, 16, size=(n, k // g))
+    scale = (rng.random((n, k // g)) * 0.01 + 1e-3).astype(np.float16)
+    gidx = rng.permutation(np.repeat(np.arange(k // g), g)) if use_gidx else None
+    w = {'p.weight_packed': qdq.pack_unsigned(codes, 4, 1), 'p.weight_shape': np.array([n, k]),
+         'p.weight_scale': scale}
+    if not symmetric:
+        w['p.weight_zero_point'] = qdq.pack_unsigned(zeros, 4, 0)
+    if use_gidx:
+        w['p.weight_g_idx'] = gidx.astype(np.int32)
+    got = qdq.decode_weight(w, 'p.weight', group_size=g)
+    for r in range(n):
+        for c in range(k):
+            grp = int(gidx[c]) if use_gidx else c // g
+            z = 8 if symmetric else int(zeros[r, grp])
+            want = f16((int(codes[r, c]) - z) * float(scale[r, grp]))
+            assert got[r, c] == want or (math.isnan(want) and math.isnan(got[r, c]))
+
+
+# --------------------------------------------------------------------------- INT8 quantizer
+
+@pytest.mark.parametrize('case', ['kat_int8_zero_tiny_rows', 'kat_int8_half_even', 'kat_int8_stored_scale',
+                                  'kat_int8_clamp'])
+def test_int8_quantizer_known_answers(case):
+    c = KAT[case]
+    q, s = qdq.quantize_linear_weight(np.array(c['weight'], dtype=np.float32),
+                                      row_block_size=c.get('row_block_size', 256))
+    assert q.tolist() == c['expected_q']
+    assert s.view(np.uint16).tolist() == c['expected_scale_f16_bits']
+
+
+def test_int8_quantizer_invariants():
+    # tests/test_quantization.py:21-40 with a numpy draw: rows scaled 0.02 .. 2.
+    rng = np.random.default_rng(7)
+    w = rng.standard_normal((9, 37)).astype(np.float32) * np.linspace(0.02, 2.0, 9, dtype=np.float32)[:, None]
+    qb, sb = qdq.quantize_linear_weight(w, row_block_size=2)
+    qu, su = qdq.quantize_linear_weight(w, row_block_size=9)
+    assert np.array_equal(qb, qu) and np.array_equal(sb, su)
+    assert qb.min() >= -127 and qb.max() <= 127
+    recon = qdq.dequantize_linear_weight(qb, sb).astype(np.float32)
+    assert np.all(np.abs(w - recon).max(axis=1) <= sb.astype(np.float32) * 0.6 + 2e-6)
+    assert np.all(np.abs(qb).max(axis=1) >= 126)   # the row absmax lands near the top code
+
+
+def test_int8_quantizer_errors():
+    with pytest.raises(ValueError):
+        qdq.quantize_linear_weight(np.zeros(4, dtype=np.float32))
+    with pytest.raises(TypeError):
+        qdq.quantize_linear_weight(np.zeros((2, 2), dtype=np.int32))
+    with pytest.raises(ValueError):
+        qdq.quantize_linear_weight(np.zeros((0, 2), dtype=np.float32))
+    with pytest.raises(ValueError):
+        qdq.quantize_linear_weight(np.array([[1.0, np.nan]], dtype=np.float32))
+    with pytest.raises(OverflowError):
+        qdq.quantize_linear_weight(np.array([[1e7 * 127, 1.0]], dtype=np.float32))
+    with pytest.raises(ValueError):
+        qdq.quantize_linear_weight(np.ones((2, 2), dtype=np.float32), row_block_size=0)
+
+
+# --------------------------------------------------------------------------- linear + metrics
+
+def test_linear_fp32_matches_float64_brute_force():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, 7)).astype(np.float16)
+    w = (rng.standard_normal((5, 7)) * 0.3).astype(np.float16)
+    b = rng.standard_normal(5).astype(np.float16)
+    got = qdq.linear_fp32(x, w, b)
+    assert got.shape == (3, 5)
+    for m in range(3):
+        for n in range(5):
+            ref = sum(float(x[m, j]) * float(w[n, j]) for j in range(7)) + float(b[n])
+            # fp32 vs fp64 accumulation may differ by one fp16 ulp after rounding
+            assert abs(float(got[m, n]) - float(f16(ref))) <= 2.0 ** -10 * max(abs(ref), 2.0 ** -14)
+
+
+def test_parity_metrics_closed_form():
+    m = qdq.parity_metrics(np.array([1.0, 2.0, 3.0]), np.array([1.0, 2.0, 4.0]))
+    assert m['max_abs'] == 1.0 and m['ref_inf'] == 4.0
+    assert m['mean_rel'] == pytest.approx(1 / 7)
+    assert m['relative_l2'] == pytest.approx(1 / math.sqrt(21))
+    assert m['cosine'] == pytest.approx(17 / math.sqrt(14 * 21))
+    assert not qdq.parity_ok(m)
+    assert qdq.parity_ok(qdq.parity_metrics(np.array([1.0, 2.0]), np.array([1.0, 2.0])))
+
+
+# --------------------------------------------------------------------------- tile layout model
+
+def test_nibble_order_gives_consecutive_pairs_under_the_kernel_masks():
+    rng = np.random.default_rng(5)
+    src = rng.integers(0, 2**32, size=64, dtype=np.uint64).astype(np.uint32)
+    tile = tile_layout.permute_nibbles(src)
+    for s, t in zip(src.tolist(), tile.tolist()):
+        e = [(s >> (4 * j)) & 0xF for j in range(8)]
+        lo = [t & 0x000F000F, (t & 0x00F000F0) >> 4, (t >> 8) & 0x000F000F, ((t >> 8) & 0x00F000F0) >> 4]
+        for p, v in enumerate(lo):
+            assert (v & 0xFFFF, v >> 16) == (e[2 * p], e[2 * p + 1])
+    assert np.array_equal(tile_layout.unpermute_nibbles(tile), src)
+
+
+@pytest.mark.parametrize('n,k,g,sym', [(16, 256, 128, False), (24, 512, 256, False), (40, 384, 128, True)])
+def test_w4_tile_round_trip_and_dequant(n, k, g, sym):
+    weights, _ = synth.w4_case(n, k, 1, seed=11, group_size=g, symmetric=sym, name='p.weight')
+    packed, scale = weights['p.weight_packed'], weights['p.weight_scale']
+    zero = weights.get('p.weight_zero_point')
+    tiles, meta = tile_layout.w4_repack(packed, scale, zero, n, k, g)
+    assert tiles.nbytes == (-(-n // 16) * 16) * k // 2
+    p2, s2, z2 = tile_layout.w4_unpack(tiles, meta, n, k, g)
+    assert np.array_equal(p2, packed) and np.array_equal(s2.view(np.uint16), scale.view(np.uint16))
+    if zero is None:
+        assert np.all(z2.view(np.uint32) == tile_layout.SYMMETRIC_ZERO_WORD)
+    else:
+        assert np.array_equal(z2, zero)
+    assert np.array_equal(tile_layout.w4_dequant(tiles, meta, n, k, g).view(np.uint16),
+                          qdq.decode_weight(weights, 'p.weight', group_size=g).view(np.uint16))
+
+
+def test_w8_tile_round_trip():
+    rng = np.random.default_rng(6)
+    q = rng.integers(-127, 128, size=(40, 256)).astype(np.int8)
+    s = (rng.random(40) + 0.1).astype(np.float16)
+    tiles, meta = tile_layout.w8_repack(q, s, 40, 256)
+    q2, s2 = tile_layout.w8_unpack(tiles, meta, 40, 256)
+    assert np.array_equal(q2, q) and np.array_equal(s2, s)
+
+
+# --------------------------------------------------------------------------- synthetic inputs
+
+def test_awq_synthetic_quantizer_is_valid_and_close():
+    n, k = 32, 512
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float16)
+    t = synth.awq_quantize(w)
+    assert t['weight_packed'].shape == (n, k // 8) and t['weight_packed'].dtype == np.int32
+    assert t['weight_scale'].shape == (n, k // 128) and np.all(t['weight_scale'] > 0)
+    assert t['weight_zero_point'].shape == (n // 8, k // 128)
+    dec = qdq.decode_weight(synth.prefixed(t, 'a.weight'), 'a.weight').astype(np.float32)
+    s = np.repeat(t['weight_scale'].astype(np.float32), 128, axis=1)
+    # round-to-nearest: half a step, plus the fp16 rounding of the decoded value
+    w32 = w.astype(np.float32)
+    assert np.all(np.abs(dec - w32) <= s * 0.5 + np.abs(w32) * 2.0 ** -10 + 1e-7)
