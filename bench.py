@@ -86,14 +86,10 @@ def time_graph(torch, graph, reps: int) -> float:
 
 
 def kernel_name_for(native_shape: tuple[int, int, int]) -> str:
-    """The skinny kernel instantiation the library picks for (M, N, K): mirrors
-    the host-side choice in csrc/wq_gemv.hip (pick_skinny)."""
+    """Kernel the library runs for (M, N, K): M <= 4 goes to the LDS-staged
+    decode GEMV (one instantiation for every decode shape)."""
     m, n, k = native_shape
-    ntile, nblk = (n + 15) // 16, k // 128
-    ksw = 1
-    while ksw < 16 and ntile * ksw < 2048 and nblk // (ksw * 2) >= 2:
-        ksw *= 2
-    return f'w4_skinny_kernel<1, 1, {ksw}, 4>'
+    return 'w4_gemv_lds_kernel<8>' if m <= 4 else 'w4_skinny_kernel'
 
 
 def cpu_baseline(budget_s: float) -> dict:

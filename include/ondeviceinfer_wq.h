@@ -85,8 +85,15 @@ int wq_w4_decode(const int32_t* weight_packed, const float* weight_scale,
                  int64_t n, int64_t k, int64_t num_groups, int64_t group_size,
                  uint16_t* weight, void* stream);
 
-/* Workspace bytes wq_w4a16_linear needs for this shape (may be 0).
- * Replaces marlin_make_workspace_new (backend.py:223). */
+/* Workspace bytes wq_w4a16_linear can use for this shape (0 when it needs
+ * none).  The workspace holds the per-tile counters and fp32 partials of the
+ * decode GEMV when a tile's k range is split over several workgroups.  It must
+ * be zero-filled once before first use; every call leaves it zeroed again, so
+ * it can be reused by later calls (and graph replays) on the same stream.
+ * Calls that may run concurrently need separate workspaces.  With a NULL or
+ * smaller workspace the kernels keep each tile in one workgroup (same result,
+ * slower for short-N shapes).  Replaces marlin_make_workspace_new
+ * (backend.py:223). */
 int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t group_size, size_t* bytes);
 
 /* y fp16 [m, n] = x fp16 [m, k] . dequant(W)^T with fp32 accumulation.
@@ -105,6 +112,12 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
 int wq_w8_decode(const int8_t* qweight, const float* scale, int64_t n, int64_t k,
                  uint16_t* weight, void* stream);
 
+/* Workspace bytes wq_w8a16_linear can use (same contract as
+ * wq_w4a16_workspace_size).  Replaces the fp16 dequant scratch sizing of
+ * QuantizedCpuWeightStore.max_dequant_elements (runtime/quantized.py:90-96),
+ * with far less memory. */
+int wq_w8a16_workspace_size(int64_t m, int64_t n, int64_t k, size_t* bytes);
+
 /* y fp16 [m, n] = x fp16 [m, k] . (q * scale)^T (+ bias fp16 [n] or NULL),
  * consuming the INT8 weight in its stored [n, k] row-major layout with no
  * fp16 scratch (MFMA tiles when k % 128 == 0 and x, qweight are 16-byte
@@ -113,7 +126,7 @@ int wq_w8_decode(const int8_t* qweight, const float* scale, int64_t n, int64_t k
  * (quantization.py:333-353). */
 int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight,
                     const uint16_t* scale, int64_t n, const uint16_t* bias, uint16_t* y,
-                    void* stream);
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Symmetric per-output-channel INT8 quantizer: weight fp32 [n, k] ->
  * qweight int8 [n, k] + fp16 scale [n] (absmax/127, zero rows scale 1,

@@ -47,7 +47,8 @@ _SIGNATURES = {
     'wq_w4a16_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
     'wq_w4a16_linear': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, ctypes.c_size_t, _P],
     'wq_w8_decode': [_P, _P, _I64, _I64, _P, _P],
-    'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P],
+    'wq_w8a16_workspace_size': [_I64, _I64, _I64, _SIZE_P],
+    'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
     'wq_w8_quantize': [_P, _I64, _I64, _P, _P, _P, _P],
 }
 EXPORTED_SYMBOLS = ('wq_last_error', *_SIGNATURES)
@@ -219,6 +220,34 @@ def w4a16_workspace_size(m: int, n: int, k: int, group_size: int) -> int:
     return b.value
 
 
+def w8a16_workspace_size(m: int, n: int, k: int) -> int:
+    b = ctypes.c_size_t()
+    _call('wq_w8a16_workspace_size', m, n, k, ctypes.byref(b))
+    return b.value
+
+
+_workspaces: dict = {}
+
+
+def shared_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Zero-filled workspace for callers that do not bring their own.
+
+    One buffer per device, grown on demand and never freed (a graph may have
+    captured its address).  The kernels leave it zeroed after every call, so
+    calls ordered on one stream can share it; concurrent streams need their
+    own workspace (pass ``workspace=``).
+    """
+    if nbytes <= 0:
+        return None
+    key = (device.type, device.index)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces.setdefault(('retired',) + key, []).append(_workspaces.get(key))
+        _workspaces[key] = buf
+    return buf
+
+
 def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: int, group_size: int,
                  out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """``y[m, n] = x[m, k] . dequant(W)^T`` on the repacked weight."""
@@ -233,6 +262,8 @@ def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: in
         _check(out, torch.float16, (m, n), 'out')
         if out.data_ptr() % 16:
             raise ValueError('out must be 16-byte aligned')
+    if workspace is None and m <= 4:
+        workspace = shared_workspace(device, w4a16_workspace_size(m, n, k, group_size))
     ws_ptr, ws_bytes = None, 0
     if workspace is not None:
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
@@ -257,7 +288,7 @@ def w8_decode(qweight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
 
 
 def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """``y = x . (q * scale)^T (+ bias)`` straight from the row-major INT8 weight."""
     device = _require_gpu(x, qweight, scale, bias, out)
     if x.dtype != torch.float16 or x.dim() != 2:
@@ -278,8 +309,13 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bi
         out = torch.empty((m, n), dtype=torch.float16, device=device)
     else:
         _check(out, torch.float16, (m, n), 'out')
+    if workspace is None and m <= 4:
+        workspace = shared_workspace(device, w8a16_workspace_size(m, n, k))
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     _call('wq_w8a16_linear', _ptr(x), m, k, _ptr(q), _ptr(scale.contiguous()), n,
-          _ptr(None if bias is None else bias.contiguous()), _ptr(out), _stream(device))
+          _ptr(None if bias is None else bias.contiguous()), _ptr(out), ws_ptr, ws_bytes, _stream(device))
     return out
 
 

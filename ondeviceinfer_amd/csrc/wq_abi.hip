@@ -15,10 +15,11 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
+size_t gemv_workspace_bytes(bool w4, int64_t m, int64_t n, int64_t k);
 int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
-                     half_t* y, hipStream_t s);
+                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s);
 int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
-                     half_t* y, hipStream_t s);
+                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s);
 int launch_w8_generic(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
                       half_t* y, hipStream_t s);
 int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
@@ -54,43 +55,54 @@ extern "C" int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t 
   if (int st = linear_shape_check(m, n, k)) return st;
   WQ_REQUIRE(bytes, WQ_ERR_INVALID_ARGUMENT, "null size output");
   (void)group_size;
-  *bytes = 0;  // every current kernel reduces inside its workgroup
+  *bytes = gemv_workspace_bytes(true, m, n, k);
+  return WQ_OK;
+}
+
+extern "C" int wq_w8a16_workspace_size(int64_t m, int64_t n, int64_t k, size_t* bytes) {
+  if (int st = linear_shape_check(m, n, k)) return st;
+  WQ_REQUIRE(bytes, WQ_ERR_INVALID_ARGUMENT, "null size output");
+  *bytes = k % kW8BlockK == 0 ? gemv_workspace_bytes(false, m, n, k) : 0;
   return WQ_OK;
 }
 
 extern "C" int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, const void* meta,
                                int64_t n, int64_t group_size, uint16_t* y, void* workspace, size_t workspace_bytes,
                                void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (int st = linear_shape_check(m, n, k)) return st;
   WQ_REQUIRE(n % 8 == 0 && group_size % kW4BlockK == 0 && group_size > 0 && k % group_size == 0,
              WQ_ERR_UNSUPPORTED, "W4A16 needs n %% 8 == 0, group_size %% 128 == 0, k %% group_size == 0 "
              "(n=%lld k=%lld group=%lld)", (long long)n, (long long)k, (long long)group_size);
-  WQ_REQUIRE(x && tiles && meta && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(tiles && meta, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (m == 0) return WQ_OK;   // empty activations: x and y may be null
+  WQ_REQUIRE(x && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
   WQ_REQUIRE(aligned16(x) && aligned16(tiles) && aligned16(y) && (reinterpret_cast<uintptr_t>(meta) & 7u) == 0,
              WQ_ERR_INVALID_ARGUMENT, "x, tiles and y must be 16-byte aligned and meta 8-byte aligned");
-  if (m == 0) return WQ_OK;
   const half_t* xh = reinterpret_cast<const half_t*>(x);
   half_t* yh = reinterpret_cast<half_t*>(y);
   if (m <= kSkinnyMaxM)
     return launch_w4_skinny(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
-                            reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
+                            reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, workspace,
+                            workspace_bytes, as_stream(stream));
   return launch_w4_gemm(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
                         reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
 }
 
 extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight, const uint16_t* scale,
-                               int64_t n, const uint16_t* bias, uint16_t* y, void* stream) {
+                               int64_t n, const uint16_t* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
+                               void* stream) {
   if (int st = linear_shape_check(m, n, k)) return st;
-  WQ_REQUIRE(x && qweight && scale && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
-  if (m == 0) return WQ_OK;
+  WQ_REQUIRE(qweight && scale, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (m == 0) return WQ_OK;   // empty activations: x and y may be null
+  WQ_REQUIRE(x && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
   const half_t* xh = reinterpret_cast<const half_t*>(x);
   const half_t* sh = reinterpret_cast<const half_t*>(scale);
   const half_t* bh = reinterpret_cast<const half_t*>(bias);
   half_t* yh = reinterpret_cast<half_t*>(y);
   if (k % kW8BlockK != 0 || !aligned16(x) || !aligned16(qweight))
     return launch_w8_generic(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
-  if (m <= kSkinnyMaxM) return launch_w8_skinny(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
+  if (m <= kSkinnyMaxM)
+    return launch_w8_skinny(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, workspace, workspace_bytes,
+                            as_stream(stream));
   return launch_w8_gemm(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
 }

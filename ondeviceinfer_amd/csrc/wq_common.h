@@ -28,6 +28,9 @@ typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 constexpr int kW4BlockK = 128;     // k extent of one W4 tile block (one 1 KiB wave load)
 constexpr int kW4MetaBytes = 40;   // per (16-row tile, group): 16 fp16 scales + 2 zero words
 constexpr int kW8BlockK = 128;     // k extent of one INT8 wave block (2 x 16 B per lane)
+// Word 3 of a gfx9 buffer resource: 32-bit data format, so raw dword loads
+// are range-checked against num_records and return 0 past it.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 __device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
@@ -41,6 +44,15 @@ __device__ __forceinline__ void w4_zero_consts(uint32_t z, uint32_t& c_lo, uint3
   c_hi = (zz << 4) | 0xD400D400u;
 }
 
+// (a & mask) | c in one VALU op.  gfx9 VOP3 cannot take two literal
+// operands, so the compiler splits the expression into v_and + v_or; this
+// keeps the mask in an SGPR and the OR-constant in a (hoisted) VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(c));
+  return r;
+}
+
 // One tile word (nibble p holds element {0,2,4,6,1,3,5,7}[p]) -> the eight
 // exact fp16 values (q_e - z), e = 0..7 in order.  OR-ing a nibble into the
 // mantissa of 1024.0 gives 1024+q exactly; the high nibble of each byte lands
@@ -48,10 +60,10 @@ __device__ __forceinline__ void w4_zero_consts(uint32_t z, uint32_t& c_lo, uint3
 __device__ __forceinline__ half8_t w4_word_to_h8(uint32_t w, uint32_t c_lo, uint32_t c_hi) {
   const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
   const uint32_t w8 = w >> 8;
-  const half2_t t0 = as_h2((w & 0x000F000Fu) | 0x64006400u);
-  const half2_t t1 = as_h2((w & 0x00F000F0u) | 0x64006400u);
-  const half2_t t2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u);
-  const half2_t t3 = as_h2((w8 & 0x00F000F0u) | 0x64006400u);
+  const half2_t t0 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u));
+  const half2_t t1 = as_h2(and_or(w, 0x00F000F0u, 0x64006400u));
+  const half2_t t2 = as_h2(and_or(w8, 0x000F000Fu, 0x64006400u));
+  const half2_t t3 = as_h2(and_or(w8, 0x00F000F0u, 0x64006400u));
   const half2_t p0 = t0 + as_h2(c_lo);
   const half2_t p1 = __builtin_elementwise_fma(t1, sixteenth, as_h2(c_hi));
   const half2_t p2 = t2 + as_h2(c_lo);

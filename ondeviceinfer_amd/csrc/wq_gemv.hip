@@ -14,6 +14,8 @@
 #include "wq_common.h"
 #include "wq_status.h"
 
+#include <stdlib.h>
+
 namespace wq {
 namespace {
 
@@ -241,6 +243,214 @@ __global__ __launch_bounds__(64 * KSW) void w8_skinny_kernel(const half_t* __res
   });
 }
 
+// Decode GEMV for M <= MM (MM = 1 or 4), W4 tiles or INT8 row-major weights.
+//
+// One workgroup per 16-row tile; its ksw waves split the tile's K/128
+// blocks: every wave owns NB consecutive blocks and the first `extra` waves
+// one more (NB is a template parameter, so the bulk of the loads is
+// straight-line code).  A wave first loads its slice of x[M, K] and (W4) the
+// scale/zero records of its groups, then issues all its weight loads
+// (non-temporal) before consuming any of them, in order, each behind an exact
+// vmcnt.  x and the records go to a wave-private LDS region, so the only
+// workgroup barrier is the final cross-wave sum.  Rows m >= M read row M-1
+// (in bounds) and are never stored; reads past the end of x are clamped.
+enum class WFmt { W4, W8 };
+
+// Widest workgroup (in waves) each instantiation is compiled for: the
+// register budget of a 1024-thread group (128 VGPRs) holds about 12 W4 or 8
+// INT8 blocks per wave.
+template <int NB, WFmt F>
+constexpr int flat_max_ksw() { return NB <= (F == WFmt::W4 ? 12 : 8) ? 16 : 8; }
+
+template <WFmt F>
+struct BlockRegs;
+template <>
+struct BlockRegs<WFmt::W4> { uint4_t w; };
+template <>
+struct BlockRegs<WFmt::W8> { uint4_t a, b; };
+
+// k offset (in halves, inside one 128-k block) of MFMA step w for lane slot kb.
+template <WFmt F>
+__device__ __forceinline__ int blk_kcol(int kb, int w) {
+  return F == WFmt::W4 ? kb * 32 + 8 * w : kb * 16 + 8 * (w & 1) + 64 * (w >> 1);
+}
+
+template <int NB, int MM, WFmt F>
+__global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel(
+    const half_t* __restrict__ x, int M, int K, const void* __restrict__ wsrc, const void* __restrict__ wmeta,
+    const half_t* __restrict__ bias, int N, int g_shift, half_t* __restrict__ y, int S,
+    float4_t* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int NBX = NB + 1;                                // staged slice length (blocks)
+  constexpr int kXChunks = MM * NBX * 16;                    // 16 B chunks of the x slice
+  constexpr int kXPerLane = (kXChunks + 63) / 64;
+  constexpr int kXBytes = kXPerLane * 64 * 16;
+  constexpr int kMetaChunks = F == WFmt::W4 ? (NBX + 1) * kW4MetaBytes / 8 : 0;
+  constexpr int kMPerLane = (kMetaChunks + 63) / 64;
+  constexpr int kWaveBytes = kXBytes + kMPerLane * 64 * 8;
+  const int ksw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15, kb = lane >> 4;
+  const int tile = blockIdx.x;
+  const int nblk = K / kW4BlockK;
+  const int split = blockIdx.y;                               // k range [base, base + nblk_s) of S
+  const int base = (split * nblk) / S;
+  const int nblk_s = ((split + 1) * nblk) / S - base;
+  const int extra = nblk_s - NB * ksw;                        // 0 <= extra <= ksw
+  const bool more = wave < extra;
+  const int b0 = base + wave * NB + min(wave, extra);
+  uint8_t* wl = smem + wave * kWaveBytes;
+  half_t* xl = reinterpret_cast<half_t*>(wl);
+  uint8_t* ml = wl + kXBytes;
+
+  // 1) x slice (and the W4 records): small, mostly L2 hits.
+  uint4_t xr[kXPerLane];
+#pragma unroll
+  for (int j = 0; j < kXPerLane; ++j) {
+    const int c = min(lane + 64 * j, kXChunks - 1);
+    const int m = min(c / (NBX * 16), M - 1);
+    const int off = min(b0 * kW4BlockK + (c % (NBX * 16)) * 8, K - 8);
+    xr[j] = *reinterpret_cast<const uint4_t*>(x + (size_t)m * K + off);
+  }
+  int g_lo = 0;
+  uint2_t mr[kMPerLane > 0 ? kMPerLane : 1];
+  if constexpr (F == WFmt::W4) {
+    const int ngrp = nblk >> g_shift;
+    g_lo = b0 >> g_shift;
+    const int g_hi = min((b0 + NB) >> g_shift, ngrp - 1);
+    const int meta_chunks = (g_hi - g_lo + 1) * (kW4MetaBytes / 8);
+    const uint2_t* mg = reinterpret_cast<const uint2_t*>(reinterpret_cast<const uint8_t*>(wmeta) +
+                                                         ((size_t)tile * ngrp + g_lo) * kW4MetaBytes);
+#pragma unroll
+    for (int j = 0; j < kMPerLane; ++j) mr[j] = mg[min(lane + 64 * j, meta_chunks - 1)];
+  }
+
+  // 2) all of this wave's weight blocks, before any is used.
+  BlockRegs<F> wv[NBX];
+  const int ntile = (N + 15) >> 4;
+  if constexpr (F == WFmt::W4) {
+    const uint4_t* wp = reinterpret_cast<const uint4_t*>(wsrc) + ((size_t)tile * nblk + b0) * 64 + lane;
+#pragma unroll
+    for (int s2 = 0; s2 < NB; ++s2) wv[s2].w = __builtin_nontemporal_load(wp + s2 * 64);
+    if (more) wv[NB].w = __builtin_nontemporal_load(wp + NB * 64);
+  } else {
+    const int row = min(tile * 16 + i, N - 1);
+    const uint4_t* wp = reinterpret_cast<const uint4_t*>(reinterpret_cast<const int8_t*>(wsrc) + (size_t)row * K +
+                                                         (size_t)b0 * kW8BlockK + 16 * kb);
+#pragma unroll
+    for (int s2 = 0; s2 < NB; ++s2) {
+      wv[s2].a = __builtin_nontemporal_load(wp + s2 * 8);
+      wv[s2].b = __builtin_nontemporal_load(wp + s2 * 8 + 4);
+    }
+    if (more) {
+      wv[NB].a = __builtin_nontemporal_load(wp + NB * 8);
+      wv[NB].b = __builtin_nontemporal_load(wp + NB * 8 + 4);
+    }
+  }
+  (void)ntile;
+
+  // 3) park x and the records in this wave's LDS region (every lane stores,
+  //    so the loads above stay ahead of the weight loads).
+#pragma unroll
+  for (int j = 0; j < kXPerLane; ++j) reinterpret_cast<uint4_t*>(xl)[lane + 64 * j] = xr[j];
+  if constexpr (F == WFmt::W4) {
+#pragma unroll
+    for (int j = 0; j < kMPerLane; ++j) reinterpret_cast<uint2_t*>(ml)[lane + 64 * j] = mr[j];
+  }
+
+  const bool has_x = i < M;
+  half8_t xv[4] = {half8_t{}, half8_t{}, half8_t{}, half8_t{}};   // columns m >= M stay zero
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int s2) {
+    if (has_x) {
+      const half_t* xp = xl + (i * NBX + s2) * kW4BlockK;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) xv[w] = ld_h8(xp + blk_kcol<F>(kb, w));
+    }
+    if constexpr (F == WFmt::W4) {
+      const uint8_t* rec = ml + (((b0 + s2) >> g_shift) - g_lo) * kW4MetaBytes;
+      const uint2_t sc = *reinterpret_cast<const uint2_t*>(rec + 8 * kb);
+      const uint32_t zw = *reinterpret_cast<const uint32_t*>(rec + 32 + 4 * (i >> 3));
+      uint32_t c_lo, c_hi;
+      w4_zero_consts((zw >> (4 * (i & 7))) & 0xFu, c_lo, c_hi);
+      float4_t cg = {0.f, 0.f, 0.f, 0.f};
+      cg = mfma16(w4_word_to_h8(wv[s2].w.x, c_lo, c_hi), xv[0], cg);
+      cg = mfma16(w4_word_to_h8(wv[s2].w.y, c_lo, c_hi), xv[1], cg);
+      cg = mfma16(w4_word_to_h8(wv[s2].w.z, c_lo, c_hi), xv[2], cg);
+      cg = mfma16(w4_word_to_h8(wv[s2].w.w, c_lo, c_hi), xv[3], cg);
+      const half4_t s4 = __builtin_bit_cast(half4_t, sc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] += (float)s4[v] * cg[v];
+    } else {
+      acc = mfma16(i8x8_to_h8(wv[s2].a.x, wv[s2].a.y), xv[0], acc);
+      acc = mfma16(i8x8_to_h8(wv[s2].a.z, wv[s2].a.w), xv[1], acc);
+      acc = mfma16(i8x8_to_h8(wv[s2].b.x, wv[s2].b.y), xv[2], acc);
+      acc = mfma16(i8x8_to_h8(wv[s2].b.z, wv[s2].b.w), xv[3], acc);
+    }
+  };
+#pragma unroll
+  for (int s2 = 0; s2 < NB; ++s2) consume(s2);
+  if (more) consume(NB);
+
+  float4_t* red = reinterpret_cast<float4_t*>(smem + ksw * kWaveBytes);
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  float4_t sum = red[lane];
+  for (int w2 = 1; w2 < ksw; ++w2) sum += red[w2 * 64 + lane];
+  if (S > 1) {
+    // Cross-workgroup sum over the S k-splits of this tile: every split
+    // publishes its partial, the last to arrive adds them in split order (so
+    // the result does not depend on arrival order) and re-arms the counter.
+    // Partials and counter are only touched with device-scope atomics, which
+    // are coherent across the XCDs' L2s by themselves; the vmcnt(0) wait
+    // orders the partial's stores before the counter increment.  A fence
+    // here would write back and invalidate the whole L2 in every workgroup.
+    float* mine = reinterpret_cast<float*>(ws_part + ((size_t)tile * S + split) * 64 + lane);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) __hip_atomic_store(mine + v, sum[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    uint32_t prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != (uint32_t)(S - 1)) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const float* all = reinterpret_cast<const float*>(ws_part + (size_t)tile * S * 64 + lane);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sum[v] = __hip_atomic_load(all + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int s2 = 1; s2 < S; ++s2) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sum[v] += __hip_atomic_load(all + s2 * 256 + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (has_x) {
+    const int n0 = tile * 16 + 4 * kb;
+    if constexpr (F == WFmt::W4) {
+      if (n0 < N) {
+        half4_t o;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = (half_t)sum[v];
+        *reinterpret_cast<half4_t*>(y + (size_t)i * N + n0) = o;
+      }
+    } else {
+      const half_t* scale = reinterpret_cast<const half_t*>(wmeta);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int n = n0 + v;
+        if (n < N) {
+          float r = sum[v] * (float)scale[n];
+          if (bias) r += (float)bias[n];
+          y[(size_t)i * N + n] = (half_t)r;
+        }
+      }
+    }
+  }
+}
+
 // Any-shape INT8 x fp16 linear: one wavefront per output (m, n), lanes
 // stride over k, fp32 accumulation, row scale applied at the end.  Serves
 // shapes the tiled kernels do not take (k % 128 != 0 or unaligned operands).
@@ -345,10 +555,120 @@ int launch_w8_skinny_k(int ksw, const half_t* x, int M, int K, const int8_t* q, 
   }
 }
 
+constexpr int kGemvFlatMaxM = 4;
+constexpr int kGemvMaxBytes = 64 * 1024;
+constexpr int kNotApplicable = -1;
+constexpr int kFlatMaxNB = 16;
+
+template <int NB, int MM, WFmt F>
+constexpr int flat_lds_bytes(int ksw) {
+  const int x = ((MM * (NB + 1) * 16 + 63) / 64) * 64 * 16;
+  const int m = F == WFmt::W4 ? (((NB + 2) * kW4MetaBytes / 8 + 63) / 64) * 64 * 8 : 0;
+  return ksw * (x + m) + ksw * 1024;
+}
+
+struct FlatPlan {
+  int split, ksw;
+};
+
+int env_int(const char* name) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : 0;
+}
+
+// Work split for the flat GEMV: S workgroups per tile along k when the tile
+// count alone would leave the machine under-filled, and ksw waves per
+// workgroup targeting ~4 blocks per wave (at most 12 waves, so two or more
+// workgroups fit per CU).  WQ_GEMV_SPLIT / WQ_GEMV_KSW override it in tuning
+// runs.
+template <WFmt F>
+FlatPlan plan_flat(int ntile, int nblk, bool may_split = true) {
+  FlatPlan p{1, 1};
+  if (ntile < 128 && nblk >= 16) p.split = 4;
+  else if (ntile < 512 && nblk >= 64) p.split = 2;
+  const int fs = env_int("WQ_GEMV_SPLIT");
+  if (fs == 1 || fs == 2 || fs == 4 || fs == 8) p.split = fs;
+  if (p.split > nblk || !may_split) p.split = 1;
+  const int per = nblk / p.split;
+  int ksw = (per + 3) / 4;
+  if (ksw > 12) ksw = 12;
+  const int fk = env_int("WQ_GEMV_KSW");
+  if (fk >= 1 && fk <= 16) ksw = fk;
+  if (ksw > per) ksw = per;
+  if (ksw < 1) ksw = 1;
+  const int limit = per / ksw <= (F == WFmt::W4 ? 12 : 8) ? 16 : 8;
+  p.ksw = ksw > limit ? limit : ksw;
+  return p;
+}
+
+size_t flat_workspace_bytes(int ntile, int split) {
+  if (split <= 1) return 0;
+  return (((size_t)ntile * 4 + 255) & ~(size_t)255) + (size_t)ntile * split * 64 * sizeof(float4_t);
+}
+
+template <int NB, int MM, WFmt F>
+int launch_flat(const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias, int N,
+                int g_shift, half_t* y, FlatPlan p, void* ws, hipStream_t s) {
+  if (p.ksw > flat_max_ksw<NB, F>()) return kNotApplicable;
+  const int lds = flat_lds_bytes<NB, MM, F>(p.ksw);
+  if (lds > kGemvMaxBytes) return kNotApplicable;
+  const int ntile = (N + 15) / 16;
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(ws);
+  float4_t* part = p.split > 1 ? reinterpret_cast<float4_t*>(reinterpret_cast<uint8_t*>(ws) +
+                                                             (((size_t)ntile * 4 + 255) & ~(size_t)255))
+                               : nullptr;
+  hipLaunchKernelGGL((gemv_flat_kernel<NB, MM, F>), dim3((unsigned)ntile, (unsigned)p.split), dim3(64 * p.ksw), lds,
+                     s, x, M, K, w, meta, bias, N, g_shift, y, p.split, part, cnt);
+  return check_launch(F == WFmt::W4 ? "w4_gemv_flat" : "w8_gemv_flat");
+}
+
+template <int MM, WFmt F, int NB = 1>
+int launch_flat_nb(int nb, const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias,
+                   int N, int g_shift, half_t* y, FlatPlan p, void* ws, hipStream_t s) {
+  if constexpr (NB > kFlatMaxNB) {
+    return kNotApplicable;
+  } else {
+    if (nb == NB) return launch_flat<NB, MM, F>(x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
+    return launch_flat_nb<MM, F, NB + 1>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
+  }
+}
+
+template <WFmt F>
+int launch_gemv_flat(const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias, int N,
+                     int g_shift, half_t* y, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int nblk = K / kW4BlockK, ntile = (N + 15) / 16;
+  FlatPlan p = plan_flat<F>(ntile, nblk);
+  // Without enough workspace the tile's k range stays in one workgroup.
+  if (p.split > 1 && (ws == nullptr || ws_bytes < flat_workspace_bytes(ntile, p.split)))
+    p = plan_flat<F>(ntile, nblk, false);
+  const int nb = (nblk / p.split) / p.ksw;
+  if (nb < 1 || nb > kFlatMaxNB) return kNotApplicable;
+  if (M == 1) return launch_flat_nb<1, F>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
+  return launch_flat_nb<4, F>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
+}
+
+int launch_w4_gemv_flat(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
+                        half_t* y, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int bpg = G / kW4BlockK;
+  if (bpg & (bpg - 1)) return kNotApplicable;     // group must be 128 * 2^j
+  return launch_gemv_flat<WFmt::W4>(x, M, K, tiles, meta, nullptr, N, __builtin_ctz(bpg), y, ws, ws_bytes, s);
+}
+
 }  // namespace
 
+size_t gemv_workspace_bytes(bool w4, int64_t m, int64_t n, int64_t k) {
+  if (m > kGemvFlatMaxM) return 0;
+  const int ntile = (int)((n + 15) / 16), nblk = (int)(k / kW4BlockK);
+  const FlatPlan p = w4 ? plan_flat<WFmt::W4>(ntile, nblk) : plan_flat<WFmt::W8>(ntile, nblk);
+  return flat_workspace_bytes(ntile, p.split);
+}
+
 int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
-                     half_t* y, hipStream_t s) {
+                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (M <= kGemvFlatMaxM) {
+    int rc = launch_w4_gemv_flat(x, M, K, tiles, meta, N, G, y, ws, ws_bytes, s);
+    if (rc != kNotApplicable) return rc;
+  }
   const int mc = (M + 15) / 16;
   const SkinnyCfg c = pick_skinny((N + 15) / 16, K / kW4BlockK, mc);
   switch (mc) {
@@ -360,7 +680,11 @@ int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const 
 }
 
 int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
-                     half_t* y, hipStream_t s) {
+                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (M <= kGemvFlatMaxM) {
+    int rc = launch_gemv_flat<WFmt::W8>(x, M, K, q, scale, bias, N, 0, y, ws, ws_bytes, s);
+    if (rc != kNotApplicable) return rc;
+  }
   const int mc = (M + 15) / 16;
   const SkinnyCfg c = pick_skinny((N + 15) / 16, K / kW8BlockK, mc);
   switch (mc) {

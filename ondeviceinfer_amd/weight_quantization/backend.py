@@ -291,7 +291,7 @@ class CompressedLinearBackend:
             tiles, meta = _native.w4_repack(packed.contiguous(), scale,
                                             None if zero is None else zero.contiguous(), n, k, self.group_size)
             ws_bytes = _native.w4a16_workspace_size(1, n, k, self.group_size)
-            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=packed.device) if ws_bytes else None
+            workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=packed.device) if ws_bytes else None
             layer[prefix + '._prepared'] = PreparedW4(tiles, meta, workspace, k, n, self.group_size)
             # The fused path retains only the repacked weights (backend.py:224-226).
             for suffix in ('.weight_packed', '.weight_scale', '.weight_zero_point'):

@@ -114,6 +114,19 @@ def test_w4a16_linear_parity_small(gpu, m, n, k):
     check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 m={m} n={n} k={k}')
 
 
+@pytest.mark.parametrize('ksw,split', [('1', '1'), ('3', '1'), ('16', '1'), ('3', '2'), ('2', '4')])
+def test_w4a16_decode_wave_split_override(gpu, monkeypatch, ksw, split):
+    """Uneven block counts per wave and per k-split (tuning overrides)."""
+    monkeypatch.setenv('WQ_GEMV_KSW', ksw)
+    monkeypatch.setenv('WQ_GEMV_SPLIT', split)
+    name = 'p.weight'
+    for m in (1, 3):
+        weights, x = synth.w4_case(1000, 1024, m, seed=int(ksw) + m, name=name)
+        backend, layer = prepared_w4(weights, name, gpu)
+        y = backend.linear(dev(x, gpu), layer, name)
+        check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 ksw={ksw} split={split} m={m}')
+
+
 def test_w4a16_group_256_and_symmetric(gpu):
     for g, sym in ((256, False), (128, True)):
         weights, x = synth.w4_case(256, 2048, 3, seed=g, group_size=g, symmetric=sym, name='p.weight')
@@ -170,6 +183,51 @@ def test_w4a16_repeat_calls_are_bitwise_identical(gpu):
             assert torch.equal(backend.linear(xd, layer, name), first)
 
 
+def test_w4a16_split_k_workspace_contract(gpu):
+    """Tiles split over several workgroups need the workspace; without one the
+    same result comes from one workgroup per tile."""
+    name = 'mlp.down_proj.weight'
+    weights, x = synth.w4_case(1024, 17408, 2, seed=12, name=name)
+    backend, layer = prepared_w4(weights, name, gpu)
+    prep = layer['mlp.down_proj._prepared']
+    need = _native.w4a16_workspace_size(1, 1024, 17408, 128)
+    assert need > 0 and prep.workspace is not None and prep.workspace.numel() >= need
+    expected = qdq.qdq_linear(x, weights, name)
+    xd = dev(x, gpu)
+    with_ws = host(_native.w4a16_linear(xd, prep.tiles, prep.meta, 1024, 128, workspace=prep.workspace))
+    tiny = torch.zeros(16, dtype=torch.uint8, device=gpu)
+    without = host(_native.w4a16_linear(xd, prep.tiles, prep.meta, 1024, 128, workspace=tiny))
+    check_parity(with_ws, expected, 'split with workspace')
+    check_parity(without, expected, 'split fallback')
+    counters = prep.workspace[:((1024 // 16) * 4 + 255) // 256 * 256]
+    assert torch.count_nonzero(counters).item() == 0      # per-tile counters re-armed
+
+
+def test_w4a16_graph_replays_match_eager(gpu):
+    """HIP-graph capture of decode GEMVs (split and unsplit shapes), replayed
+    several times with eager work in between; every replay equals eager."""
+    cases = []
+    for i, (k, n) in enumerate(((17408, 5120), (5120, 1024), (5120, 5120))):
+        name = f'l{i}.weight'
+        weights, x = synth.w4_case(n, k, 1, seed=30 + i, name=name)
+        backend, layer = prepared_w4(weights, name, gpu)
+        cases.append((backend, layer, name, dev(x, gpu), torch.empty(1, n, dtype=torch.float16, device=gpu)))
+    eager = [b.linear(x, l, nm).clone() for b, l, nm, x, _ in cases]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for b, l, nm, x, out in cases:
+            b.ops.w4a16_linear(x, l[nm.removesuffix('.weight') + '._prepared'], out)
+    for _ in range(4):
+        for _, _, _, _, out in cases:
+            out.fill_(float('nan'))
+        graph.replay()
+        torch.cuda.synchronize()
+        for (_, _, _, _, out), ref in zip(cases, eager):
+            assert torch.equal(out, ref)
+        torch.cuda.synchronize()
+
+
 def test_backend_shapes_counters_and_row_split(gpu, monkeypatch):
     name = 'self_attn.o_proj.weight'
     weights, x = synth.w4_case(512, 1024, 24, seed=8, name=name)
@@ -217,6 +275,13 @@ def test_w8a16_linear_parity(gpu, m, n, k):
     _, q, s, x = synth.int8_case(n, k, m, seed=m + n)
     y = _native.w8a16_linear(dev(x, gpu), dev(q, gpu), dev(s, gpu))
     check_parity(host(y), int8_ref(x, q, s), f'w8 m={m} n={n} k={k}')
+
+
+@pytest.mark.parametrize('m', [1, 4])
+def test_w8a16_down_shape_split(gpu, m):
+    _, q, s, x = synth.int8_case(5120, 17408, m, seed=40 + m)
+    y = _native.w8a16_linear(dev(x, gpu), dev(q, gpu), dev(s, gpu))
+    check_parity(host(y), int8_ref(x, q, s), f'w8 down m={m}')
 
 
 def test_w8a16_config1_and_bias_and_generic_shapes(gpu):
