@@ -37,6 +37,13 @@ struct WRegs<GFmt::W8, NT> {
   uint4_t a[NT], b[NT];
 };
 
+// 16 bytes per lane global -> LDS (global_load_lds_dwordx4): lane L's bytes
+// land at lds_base + 16 * L.  Kept out of the kernel template: with the
+// builtin written inside it, the host pass drops the kernel's launch stub.
+__device__ __forceinline__ void lds_load16(const void* src, uint8_t* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
+
 // LDS slot (16-byte chunk index inside a 256-byte row) of chunk c in row r.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 15); }
 
@@ -73,7 +80,7 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
       const int c = swz(r, lane & 15);
       const int row = min(m0 + r, M - 1);
       const half_t* src = x + (size_t)row * K + (size_t)blk * kW4BlockK + c * 8;
-      __builtin_amdgcn_global_load_lds(src, xs + st * kStageBytes + J * 1024, 16, 0, 0);
+      lds_load16(src, xs + st * kStageBytes + J * 1024);
     }
   };
 
