@@ -85,11 +85,42 @@ def time_graph(torch, graph, reps: int) -> float:
     return start.elapsed_time(end) / 1000.0 / reps
 
 
+def flat_plan(n: int, k: int) -> tuple[int, int, int]:
+    """(split, waves per workgroup, blocks per wave) the library picks for a
+    W4 decode GEMV at M <= 4 with the workspace supplied: a restatement of
+    plan_flat() in ondeviceinfer_amd/csrc/wq_gemv.hip, used only to name the
+    kernel instantiation in the report."""
+    ntile, nblk = (n + 15) // 16, k // 128
+    split = 4 if ntile < 512 and nblk >= 64 else 1
+    if split > nblk:
+        split = 1
+    per = nblk // split
+    ksw = 4 if split > 1 or ntile >= 1024 else 12
+    ksw = max(1, min(ksw, per))
+    limit = 16 if per // ksw <= 12 else 8
+    ksw = min(ksw, limit)
+    return split, ksw, per // ksw
+
+
 def kernel_name_for(native_shape: tuple[int, int, int]) -> str:
-    """Kernel the library runs for (M, N, K): M <= 4 goes to the LDS-staged
-    decode GEMV (one instantiation for every decode shape)."""
+    """Kernel the library runs for (M, N, K): M <= 4 goes to the decode GEMV
+    gemv_flat_kernel<NB, MM, W4> (NB = k blocks per wave, MM = 1 or 4)."""
     m, n, k = native_shape
-    return 'w4_gemv_lds_kernel<8>' if m <= 4 else 'w4_skinny_kernel'
+    if m > 4:
+        return 'w4_skinny_kernel' if m <= 64 else 'wq_gemm_kernel'
+    _, _, nb = flat_plan(n, k)
+    return f'gemv_flat_kernel<{nb}, {1 if m == 1 else 4}, W4>'
+
+
+def profiled_traffic(kernel: str, shape: str):
+    """HBM bytes per launch of `kernel` at `shape` from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by
+    its copy-kernel calibration factor), or None when none was recorded."""
+    f = ROOT / 'profiles' / 'decode_gemv_traffic.json'
+    if not f.exists():
+        return None
+    rec = json.loads(f.read_text()).get('kernels', {}).get(f'{kernel} @ {shape}')
+    return None if rec is None else int(rec['hbm_bytes_per_launch'])
 
 
 def cpu_baseline(budget_s: float) -> dict:
@@ -221,9 +252,12 @@ def main() -> int:
             agg['launches'] += e['launches_per_step']
         dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]['us'])
         achieved = dom['bytes'] / (dom['us'] / 1e6) / 1e9
+        dom_shapes = [e['shape'] for e in by_shape if e['kernel'] == dom_name]
+        traffic = profiled_traffic(dom_name, dom_shapes[0]) if len(dom_shapes) == 1 else None
         result['roofline'] = {
             'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-            'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'kernel': dom_name,
+            'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'kernel': dom_name,
+            'shapes': dom_shapes,
             'avg_launch_us': round(dom['us'] / dom['launches'], 3),
             'algorithmic_bytes_per_launch': dom['bytes'] // dom['launches'],
         }

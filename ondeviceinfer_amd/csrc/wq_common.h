@@ -73,6 +73,43 @@ __device__ __forceinline__ half8_t w4_word_to_h8(uint32_t w, uint32_t c_lo, uint
   return r;
 }
 
+// One tile word -> the eight fp16 values before the zero point is taken off:
+// 1024+q_e for e in {0,1,4,5} and 1024+16q_e for e in {2,3,6,7}.  Four VALU
+// ops per word; the caller pairs the fragment with x pre-divided by 16 at
+// e in {2,3,6,7} and with w4_zero_frag() on the same x, so that
+//   raw . x' + zero_frag . x' = sum_e (q_e - z) x_e.
+// Every product is exact in fp32 (11 x 11 significant bits).
+__device__ __forceinline__ half8_t w4_word_to_h8_raw(uint32_t w) {
+  const uint32_t w8 = w >> 8;
+  half8_t r;
+  r.s01 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u));
+  r.s23 = as_h2(and_or(w, 0x00F000F0u, 0x64006400u));
+  r.s45 = as_h2(and_or(w8, 0x000F000Fu, 0x64006400u));
+  r.s67 = as_h2(and_or(w8, 0x00F000F0u, 0x64006400u));
+  return r;
+}
+
+// The matching zero-point fragment of one row: -(1024 + z) at e in {0,1,4,5},
+// -(1024 + 16z) at e in {2,3,6,7} (exponent 25, mantissa z or 16z: exact).
+__device__ __forceinline__ half8_t w4_zero_frag(uint32_t z) {
+  const uint32_t zz = z * 0x00010001u;
+  const half2_t lo = as_h2(zz | 0xE400E400u);
+  const half2_t hi = as_h2((zz << 4) | 0xE400E400u);
+  half8_t r;
+  r.s01 = lo; r.s23 = hi; r.s45 = lo; r.s67 = hi;
+  return r;
+}
+
+// x chunk of eight consecutive k (8-aligned) -> the B fragment that pairs
+// with w4_word_to_h8_raw: elements 2,3,6,7 divided by 16 (exact for normal
+// results).
+__device__ __forceinline__ uint4_t w4_prescale_x(uint4_t v) {
+  const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
+  v.y = as_u32(as_h2(v.y) * sixteenth);
+  v.w = as_u32(as_h2(v.w) * sixteenth);
+  return v;
+}
+
 // Same, multiplied by the group scale: fp16((q - z) * s), which is the
 // reference decode bit for bit ((q - z) is exact, the product rounds once).
 __device__ __forceinline__ half8_t w4_word_to_h8_scaled(uint32_t w, uint32_t c_lo, uint32_t c_hi, half2_t s2) {
@@ -99,6 +136,27 @@ __device__ __forceinline__ half8_t i8x8_to_h8(uint32_t w0, uint32_t w1) {
   half8_t r;
   r.s0123 = i8x4_to_h4(w0);
   r.s4567 = i8x4_to_h4(w1);
+  return r;
+}
+
+// Eight signed int8 -> eight fp16 1152+q (the bias is left in; the caller
+// takes it off with one MFMA of the constant fragment kI8BiasFrag against
+// the same x).  Three VALU ops per word.
+__device__ __forceinline__ half8_t i8x8_to_h8_raw(uint32_t w0, uint32_t w1) {
+  const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+  half8_t r;
+  r.s01 = as_h2(__builtin_amdgcn_perm(u0, 0x64646464u, 0x00050004u));
+  r.s23 = as_h2(__builtin_amdgcn_perm(u0, 0x64646464u, 0x00070006u));
+  r.s45 = as_h2(__builtin_amdgcn_perm(u1, 0x64646464u, 0x00050004u));
+  r.s67 = as_h2(__builtin_amdgcn_perm(u1, 0x64646464u, 0x00070006u));
+  return r;
+}
+
+// -1152 in every element (fp16 0xE480).
+__device__ __forceinline__ half8_t i8_bias_frag() {
+  const half2_t b = as_h2(0xE480E480u);
+  half8_t r;
+  r.s01 = b; r.s23 = b; r.s45 = b; r.s67 = b;
   return r;
 }
 

@@ -249,10 +249,20 @@ __global__ __launch_bounds__(64 * KSW) void w8_skinny_kernel(const half_t* __res
 // blocks: every wave owns NB consecutive blocks and the first `extra` waves
 // one more (NB is a template parameter, so the bulk of the loads is
 // straight-line code).  A wave first loads its slice of x[M, K] and (W4) the
-// scale/zero records of its groups, then issues all its weight loads
-// (non-temporal) before consuming any of them, in order, each behind an exact
-// vmcnt.  x and the records go to a wave-private LDS region, so the only
-// workgroup barrier is the final cross-wave sum.  Rows m >= M read row M-1
+// scale/zero records of its groups, then keeps D ~ NB/2 weight blocks in
+// flight (non-temporal loads in a compile-time ring, each consumed behind an
+// exact vmcnt and refilled at once), so the math of the first blocks overlaps
+// the arrival of the rest.  x and the records go to a wave-private LDS region,
+// so the only workgroup barrier is the final cross-wave sum.
+//
+// W4 arithmetic here differs from the skinny kernels: the weights enter the
+// MFMA as 1024+q / 1024+16q (four VALU ops per word, against x with the
+// 16q positions pre-divided by 16), and four more MFMAs per block with the
+// row's zero fragment take off (1024 + z) / (1024 + 16z).  The block sum is
+// then sum_k (q - z) x up to fp32 rounding of terms ~1024|x| (relative error
+// ~1e-6 of the block), and the matrix pipe, idle at M = 1, absorbs the work
+// that would otherwise cost two more VALU ops per word.  INT8 likewise feeds
+// 1152+q and takes 1152 * x off with a constant fragment.  Rows m >= M read row M-1
 // (in bounds) and are never stored; reads past the end of x are clamped.
 enum class WFmt { W4, W8 };
 
@@ -282,6 +292,7 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel
     float4_t* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int NBX = NB + 1;                                // staged slice length (blocks)
+  constexpr int D = NB <= 3 ? NB : ((NB + 1) / 2 < 3 ? 3 : (NB + 1) / 2);   // weight blocks in flight
   constexpr int kXChunks = MM * NBX * 16;                    // 16 B chunks of the x slice
   constexpr int kXPerLane = (kXChunks + 63) / 64;
   constexpr int kXBytes = kXPerLane * 64 * 16;
@@ -326,34 +337,34 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel
     for (int j = 0; j < kMPerLane; ++j) mr[j] = mg[min(lane + 64 * j, meta_chunks - 1)];
   }
 
-  // 2) all of this wave's weight blocks, before any is used.
-  BlockRegs<F> wv[NBX];
-  const int ntile = (N + 15) >> 4;
+  // 2) the first D weight blocks (and the optional extra one) in flight
+  //    before anything is used; the rest refill the ring as it drains.
+  const uint4_t* wp;
   if constexpr (F == WFmt::W4) {
-    const uint4_t* wp = reinterpret_cast<const uint4_t*>(wsrc) + ((size_t)tile * nblk + b0) * 64 + lane;
-#pragma unroll
-    for (int s2 = 0; s2 < NB; ++s2) wv[s2].w = __builtin_nontemporal_load(wp + s2 * 64);
-    if (more) wv[NB].w = __builtin_nontemporal_load(wp + NB * 64);
+    wp = reinterpret_cast<const uint4_t*>(wsrc) + ((size_t)tile * nblk + b0) * 64 + lane;
   } else {
     const int row = min(tile * 16 + i, N - 1);
-    const uint4_t* wp = reinterpret_cast<const uint4_t*>(reinterpret_cast<const int8_t*>(wsrc) + (size_t)row * K +
-                                                         (size_t)b0 * kW8BlockK + 16 * kb);
-#pragma unroll
-    for (int s2 = 0; s2 < NB; ++s2) {
-      wv[s2].a = __builtin_nontemporal_load(wp + s2 * 8);
-      wv[s2].b = __builtin_nontemporal_load(wp + s2 * 8 + 4);
-    }
-    if (more) {
-      wv[NB].a = __builtin_nontemporal_load(wp + NB * 8);
-      wv[NB].b = __builtin_nontemporal_load(wp + NB * 8 + 4);
-    }
+    wp = reinterpret_cast<const uint4_t*>(reinterpret_cast<const int8_t*>(wsrc) + (size_t)row * K +
+                                          (size_t)b0 * kW8BlockK + 16 * kb);
   }
-  (void)ntile;
+  auto load_block = [&](BlockRegs<F>& r, int s2) {
+    if constexpr (F == WFmt::W4) {
+      r.w = __builtin_nontemporal_load(wp + s2 * 64);
+    } else {
+      r.a = __builtin_nontemporal_load(wp + s2 * 8);
+      r.b = __builtin_nontemporal_load(wp + s2 * 8 + 4);
+    }
+  };
+  BlockRegs<F> ring[D], xtra;
+#pragma unroll
+  for (int s2 = 0; s2 < D; ++s2) load_block(ring[s2], s2);
+  if (more) load_block(xtra, NB);
 
   // 3) park x and the records in this wave's LDS region (every lane stores,
   //    so the loads above stay ahead of the weight loads).
 #pragma unroll
-  for (int j = 0; j < kXPerLane; ++j) reinterpret_cast<uint4_t*>(xl)[lane + 64 * j] = xr[j];
+  for (int j = 0; j < kXPerLane; ++j)
+    reinterpret_cast<uint4_t*>(xl)[lane + 64 * j] = F == WFmt::W4 ? w4_prescale_x(xr[j]) : xr[j];
   if constexpr (F == WFmt::W4) {
 #pragma unroll
     for (int j = 0; j < kMPerLane; ++j) reinterpret_cast<uint2_t*>(ml)[lane + 64 * j] = mr[j];
@@ -362,7 +373,7 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel
   const bool has_x = i < M;
   half8_t xv[4] = {half8_t{}, half8_t{}, half8_t{}, half8_t{}};   // columns m >= M stay zero
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  auto consume = [&](int s2) {
+  auto consume = [&](const BlockRegs<F>& wb, int s2) {
     if (has_x) {
       const half_t* xp = xl + (i * NBX + s2) * kW4BlockK;
 #pragma unroll
@@ -372,26 +383,38 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel
       const uint8_t* rec = ml + (((b0 + s2) >> g_shift) - g_lo) * kW4MetaBytes;
       const uint2_t sc = *reinterpret_cast<const uint2_t*>(rec + 8 * kb);
       const uint32_t zw = *reinterpret_cast<const uint32_t*>(rec + 32 + 4 * (i >> 3));
-      uint32_t c_lo, c_hi;
-      w4_zero_consts((zw >> (4 * (i & 7))) & 0xFu, c_lo, c_hi);
+      // The zero-point terms go through the matrix pipe (they need only x
+      // and z, so they issue before the weights land); the weights take four
+      // VALU ops per word.
+      const half8_t zf = w4_zero_frag((zw >> (4 * (i & 7))) & 0xFu);
       float4_t cg = {0.f, 0.f, 0.f, 0.f};
-      cg = mfma16(w4_word_to_h8(wv[s2].w.x, c_lo, c_hi), xv[0], cg);
-      cg = mfma16(w4_word_to_h8(wv[s2].w.y, c_lo, c_hi), xv[1], cg);
-      cg = mfma16(w4_word_to_h8(wv[s2].w.z, c_lo, c_hi), xv[2], cg);
-      cg = mfma16(w4_word_to_h8(wv[s2].w.w, c_lo, c_hi), xv[3], cg);
+      cg = mfma16(zf, xv[0], cg);
+      cg = mfma16(zf, xv[1], cg);
+      cg = mfma16(zf, xv[2], cg);
+      cg = mfma16(zf, xv[3], cg);
+      cg = mfma16(w4_word_to_h8_raw(wb.w.x), xv[0], cg);
+      cg = mfma16(w4_word_to_h8_raw(wb.w.y), xv[1], cg);
+      cg = mfma16(w4_word_to_h8_raw(wb.w.z), xv[2], cg);
+      cg = mfma16(w4_word_to_h8_raw(wb.w.w), xv[3], cg);
       const half4_t s4 = __builtin_bit_cast(half4_t, sc);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] += (float)s4[v] * cg[v];
+      for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf((float)s4[v], cg[v], acc[v]);
     } else {
-      acc = mfma16(i8x8_to_h8(wv[s2].a.x, wv[s2].a.y), xv[0], acc);
-      acc = mfma16(i8x8_to_h8(wv[s2].a.z, wv[s2].a.w), xv[1], acc);
-      acc = mfma16(i8x8_to_h8(wv[s2].b.x, wv[s2].b.y), xv[2], acc);
-      acc = mfma16(i8x8_to_h8(wv[s2].b.z, wv[s2].b.w), xv[3], acc);
+      const half8_t bf = i8_bias_frag();
+#pragma unroll
+      for (int w = 0; w < 4; ++w) acc = mfma16(bf, xv[w], acc);
+      acc = mfma16(i8x8_to_h8_raw(wb.a.x, wb.a.y), xv[0], acc);
+      acc = mfma16(i8x8_to_h8_raw(wb.a.z, wb.a.w), xv[1], acc);
+      acc = mfma16(i8x8_to_h8_raw(wb.b.x, wb.b.y), xv[2], acc);
+      acc = mfma16(i8x8_to_h8_raw(wb.b.z, wb.b.w), xv[3], acc);
     }
   };
 #pragma unroll
-  for (int s2 = 0; s2 < NB; ++s2) consume(s2);
-  if (more) consume(NB);
+  for (int s2 = 0; s2 < NB; ++s2) {
+    consume(ring[s2 % D], s2);
+    if (s2 + D < NB) load_block(ring[s2 % D], s2 + D);   // compile-time condition
+  }
+  if (more) consume(xtra, NB);
 
   float4_t* red = reinterpret_cast<float4_t*>(smem + ksw * kWaveBytes);
   red[wave * 64 + lane] = acc;
@@ -576,22 +599,23 @@ int env_int(const char* name) {
   return e ? atoi(e) : 0;
 }
 
-// Work split for the flat GEMV: S workgroups per tile along k when the tile
-// count alone would leave the machine under-filled, and ksw waves per
-// workgroup targeting ~4 blocks per wave (at most 12 waves, so two or more
-// workgroups fit per CU).  WQ_GEMV_SPLIT / WQ_GEMV_KSW override it in tuning
-// runs.
+// Work split for the flat GEMV, from sweeps of the Qwen3-14B shapes on
+// MI355X.  Long-K, short-N shapes (17408 -> 5120: 320 tiles x 136 blocks)
+// split each tile's k range over four 4-wave workgroups, so the 1280
+// workgroups are all resident at once (five per CU) and every CU streams the
+// same share; one 12-wave workgroup per tile fits only once per CU at that
+// register count and leaves a second launch wave.  Otherwise one workgroup
+// per tile: 12 waves for N < 1024 tiles (enough loads in flight), 4 for wide
+// N.  WQ_GEMV_SPLIT / WQ_GEMV_KSW override it in tuning runs.
 template <WFmt F>
 FlatPlan plan_flat(int ntile, int nblk, bool may_split = true) {
   FlatPlan p{1, 1};
-  if (ntile < 128 && nblk >= 16) p.split = 4;
-  else if (ntile < 512 && nblk >= 64) p.split = 2;
+  if (ntile < 512 && nblk >= 64) p.split = 4;
   const int fs = env_int("WQ_GEMV_SPLIT");
   if (fs == 1 || fs == 2 || fs == 4 || fs == 8) p.split = fs;
   if (p.split > nblk || !may_split) p.split = 1;
   const int per = nblk / p.split;
-  int ksw = (per + 3) / 4;
-  if (ksw > 12) ksw = 12;
+  int ksw = p.split > 1 || ntile >= 1024 ? 4 : 12;
   const int fk = env_int("WQ_GEMV_KSW");
   if (fk >= 1 && fk <= 16) ksw = fk;
   if (ksw > per) ksw = per;

@@ -5,7 +5,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "../../include/ondeviceinfer_wq.h"
+#include "ondeviceinfer_wq.h"
 
 namespace wq {
 
