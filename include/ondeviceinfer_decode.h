@@ -1,0 +1,65 @@
+/* Decode-step operators around the quantized linears (batch-1 Qwen3 decode).
+ *
+ * These are the callers on either side of the quantized Linear in the
+ * reference's Qwen3 decoder layer (ondeviceinfer/quantized_model.py:124-228):
+ * residual add + RMSNorm, SiLU(gate) * up, and single-token grouped-query
+ * attention over a resident fp16 KV cache with Qwen3's per-head q/k RMSNorm,
+ * rotary embedding and the cache append folded into one launch.
+ *
+ * Same conventions as ondeviceinfer_wq.h: device pointers, fp16 as uint16_t,
+ * `stream` is a hipStream_t (may be NULL), 0 or a WQ_ERR_* code is returned and
+ * wq_last_error() holds the message, nothing allocates or synchronizes, and
+ * every call may be captured in a HIP graph.
+ */
+#ifndef ONDEVICEINFER_DECODE_H
+#define ONDEVICEINFER_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* out_sum[r] = x[r] + delta[r] (fp16 add; delta may be NULL, then x itself);
+ * out_norm[r] = weight * fp16(out_sum[r] * rsqrt(mean(out_sum[r]^2) + eps)),
+ * the reduction in fp32, for rows r < rows of n elements (n % 8 == 0).
+ * out_sum may be NULL (not written) or alias x.
+ * Replaces: `residual + attention_output` (quantized_model.py:211) followed
+ * by rms_norm (functional.py:17-22; called at quantized_model.py:147, :214). */
+int wq_add_rmsnorm(const uint16_t* x, const uint16_t* delta, const uint16_t* weight, int64_t rows, int64_t n,
+                   float eps, uint16_t* out_norm, uint16_t* out_sum, void* stream);
+
+/* out[r, i] = fp16(fp16(silu(gate_up[r, i])) * gate_up[r, n + i]) for the
+ * concatenated [gate | up] rows of a fused gate_up projection (n % 8 == 0).
+ * Replaces: `F.silu(gate) * up` (quantized_model.py:222-224). */
+int wq_silu_mul(const uint16_t* gate_up, int64_t rows, int64_t n, uint16_t* out, void* stream);
+
+/* Workspace bytes for wq_decode_attention at this geometry (zero-filled once
+ * by the caller; every call leaves it zeroed). */
+int wq_decode_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_seq,
+                                       size_t* bytes);
+
+/* One decode token of Qwen3 self-attention, batch 1, head_dim 128.
+ *   qkv          [q_heads*128 | kv_heads*128 | kv_heads*128] projection output
+ *   q/k_norm     per-head RMSNorm weights [128] (NULL: no norm)
+ *   cos/sin      RoPE tables [>= max_seq, 128] fp16, row p for position p
+ *   position     device int32: the token's position p; keys 0..p are attended
+ *   key/value_cache [kv_heads, max_seq, 128] fp16; row p is written here
+ *   out          [q_heads*128] attention output (before o_proj)
+ * Replaces: q/k rms_norm + apply_rotary_pos_emb + ResidentKVCache.update +
+ * F.scaled_dot_product_attention(enable_gqa=True) for query_length 1
+ * (quantized_model.py:171-199, layers.py:64-80, cache.py:60-80,
+ * attention.py:35-85).  A position outside [0, max_seq) writes NaN to out and
+ * leaves the cache untouched. */
+int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                        const uint16_t* q_norm_weight, const uint16_t* k_norm_weight, float eps,
+                        const uint16_t* cos_table, const uint16_t* sin_table, const int32_t* position,
+                        uint16_t* key_cache, uint16_t* value_cache, int64_t max_seq, float scale, uint16_t* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONDEVICEINFER_DECODE_H */

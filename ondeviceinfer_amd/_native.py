@@ -1,4 +1,5 @@
-"""ctypes binding of ``libondeviceinfer_wq.so`` (the C ABI in ``include/ondeviceinfer_wq.h``).
+"""ctypes binding of ``libondeviceinfer_wq.so`` (the C ABI in ``include/ondeviceinfer_wq.h``
+and ``include/ondeviceinfer_decode.h``).
 
 torch is imported first so its bundled HIP runtime (``libamdhip64.so.7``) is
 the one the library binds to: the kernels then run in torch's context and on
@@ -50,6 +51,12 @@ _SIGNATURES = {
     'wq_w8a16_workspace_size': [_I64, _I64, _I64, _SIZE_P],
     'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
     'wq_w8_quantize': [_P, _I64, _I64, _P, _P, _P, _P],
+    # include/ondeviceinfer_decode.h
+    'wq_add_rmsnorm': [_P, _P, _P, _I64, _I64, ctypes.c_float, _P, _P, _P],
+    'wq_silu_mul': [_P, _I64, _I64, _P, _P],
+    'wq_decode_attention_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
+    'wq_decode_attention': [_P, _I64, _I64, _I64, _P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _I64,
+                            ctypes.c_float, _P, _P, ctypes.c_size_t, _P],
 }
 EXPORTED_SYMBOLS = ('wq_last_error', *_SIGNATURES)
 
@@ -334,3 +341,83 @@ def w8_quantize(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     if f & 2:
         raise OverflowError('row scale is not representable in scale_dtype')
     return q, s
+
+
+# ----------------------------------------------------------------------------- decode-step operators
+
+def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: torch.Tensor | None = None,
+                out: torch.Tensor | None = None, out_sum: torch.Tensor | None = None) -> torch.Tensor:
+    """``rms_norm(x + delta)`` over the last dimension; ``out_sum`` (may be
+    ``x`` itself) receives ``x + delta``."""
+    device = _require_gpu(x, weight, delta, out, out_sum)
+    n = x.shape[-1]
+    rows = x.numel() // n if n else 0
+    for t, name in ((x, 'x'), (delta, 'delta'), (out_sum, 'out_sum')):
+        if t is not None:
+            _check(t, torch.float16, tuple(x.shape), name)
+    _check(weight, torch.float16, (n,), 'weight')
+    if out is None:
+        out = torch.empty_like(x)
+    else:
+        _check(out, torch.float16, tuple(x.shape), 'out')
+    _call('wq_add_rmsnorm', _ptr(x), _ptr(delta), _ptr(weight), rows, n, float(eps), _ptr(out), _ptr(out_sum),
+          _stream(device))
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate) * up`` of a fused ``[..., 2n]`` = ``[gate | up]`` tensor -> ``[..., n]``."""
+    device = _require_gpu(gate_up, out)
+    if gate_up.dtype != torch.float16 or not gate_up.is_contiguous() or gate_up.shape[-1] % 2:
+        raise ValueError('gate_up must be a contiguous float16 tensor with an even last dimension')
+    n = gate_up.shape[-1] // 2
+    rows = gate_up.numel() // (2 * n) if n else 0
+    shape = tuple(gate_up.shape[:-1]) + (n,)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float16, device=device)
+    else:
+        _check(out, torch.float16, shape, 'out')
+    _call('wq_silu_mul', _ptr(gate_up), rows, n, _ptr(out), _stream(device))
+    return out
+
+
+def decode_attention_workspace_size(q_heads: int, kv_heads: int, head_dim: int, max_seq: int) -> int:
+    b = ctypes.c_size_t()
+    _call('wq_decode_attention_workspace_size', q_heads, kv_heads, head_dim, max_seq, ctypes.byref(b))
+    return b.value
+
+
+def decode_attention(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: torch.Tensor | None,
+                     k_norm: torch.Tensor | None, eps: float, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                     position: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, scale: float,
+                     out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode token of GQA attention (batch 1); appends row ``position``
+    of the caches (``[kv_heads, max_seq, head_dim]`` fp16)."""
+    device = _require_gpu(qkv, q_norm, k_norm, cos_table, sin_table, position, key_cache, value_cache, out, workspace)
+    if key_cache.dim() != 3 or key_cache.shape != value_cache.shape or key_cache.shape[0] != kv_heads:
+        raise ValueError(f'caches must be [kv_heads={kv_heads}, max_seq, head_dim], got {tuple(key_cache.shape)}')
+    _, max_seq, head_dim = key_cache.shape
+    for t, name in ((key_cache, 'key_cache'), (value_cache, 'value_cache')):
+        _check(t, torch.float16, (kv_heads, max_seq, head_dim), name)
+    _check(qkv, torch.float16, ((q_heads + 2 * kv_heads) * head_dim,), 'qkv')
+    for t, name in ((q_norm, 'q_norm'), (k_norm, 'k_norm')):
+        if t is not None:
+            _check(t, torch.float16, (head_dim,), name)
+    if cos_table.dtype != torch.float16 or sin_table.dtype != torch.float16 or cos_table.shape != sin_table.shape \
+            or cos_table.dim() != 2 or cos_table.shape[1] != head_dim or cos_table.shape[0] < max_seq \
+            or not cos_table.is_contiguous() or not sin_table.is_contiguous():
+        raise ValueError(f'cos/sin tables must be contiguous float16 [>= {max_seq}, {head_dim}]')
+    _check(position, torch.int32, (1,), 'position')
+    if out is None:
+        out = torch.empty(q_heads * head_dim, dtype=torch.float16, device=device)
+    else:
+        _check(out, torch.float16, (q_heads * head_dim,), 'out')
+    need = decode_attention_workspace_size(q_heads, kv_heads, head_dim, max_seq)
+    if workspace is None and need:
+        workspace = shared_workspace(device, need)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                             workspace.numel() * workspace.element_size())
+    _call('wq_decode_attention', _ptr(qkv), q_heads, kv_heads, head_dim, _ptr(q_norm), _ptr(k_norm), float(eps),
+          _ptr(cos_table), _ptr(sin_table), _ptr(position), _ptr(key_cache), _ptr(value_cache), max_seq,
+          float(scale), _ptr(out), ws_ptr, ws_bytes, _stream(device))
+    return out

@@ -32,6 +32,24 @@ constexpr int kW8BlockK = 128;     // k extent of one INT8 wave block (2 x 16 B 
 // are range-checked against num_records and return 0 past it.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
+// Cache policy of a buffer access that is coherent across the XCDs' L2s
+// (sc1): the bits the compiler gives device-scope relaxed atomic loads and
+// stores on gfx950, here on 16-byte accesses.
+constexpr int kCoherentPolicy = 16;
+
+// 16-byte store / load at base + byte_off that other workgroups on any XCD
+// observe once the storing wave has waited for its stores (vmcnt) and
+// published that with a device-scope atomic.
+__device__ __forceinline__ void coherent_store16(void* base, uint32_t byte_off, uint4_t v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, kBufferRsrcWord3);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_off, 0, kCoherentPolicy);
+}
+__device__ __forceinline__ uint4_t coherent_load16(const void* base, uint32_t byte_off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, kBufferRsrcWord3);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCoherentPolicy);
+}
+
 __device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 

@@ -272,6 +272,13 @@ enum class WFmt { W4, W8 };
 template <int NB, WFmt F>
 constexpr int flat_max_ksw() { return NB <= (F == WFmt::W4 ? 12 : 8) ? 16 : 8; }
 
+// Waves per SIMD each instantiation must reach: the wide-N plans launch
+// about 4.25 waves per SIMD (e.g. 1088 four-wave workgroups for 5120->17408),
+// so NB <= 10 is held to 96 VGPRs (five waves per SIMD) and the whole grid is
+// resident at once instead of leaving a second launch wave.
+template <int NB, WFmt F>
+constexpr int flat_min_waves() { return NB <= (F == WFmt::W4 ? 10 : 6) ? 5 : 1; }
+
 template <WFmt F>
 struct BlockRegs;
 template <>
@@ -286,7 +293,7 @@ __device__ __forceinline__ int blk_kcol(int kb, int w) {
 }
 
 template <int NB, int MM, WFmt F>
-__global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel(
+__global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F>())) void gemv_flat_kernel(
     const half_t* __restrict__ x, int M, int K, const void* __restrict__ wsrc, const void* __restrict__ wmeta,
     const half_t* __restrict__ bias, int N, int g_shift, half_t* __restrict__ y, int S,
     float4_t* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt) {
@@ -426,13 +433,12 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel
     // Cross-workgroup sum over the S k-splits of this tile: every split
     // publishes its partial, the last to arrive adds them in split order (so
     // the result does not depend on arrival order) and re-arms the counter.
-    // Partials and counter are only touched with device-scope atomics, which
-    // are coherent across the XCDs' L2s by themselves; the vmcnt(0) wait
-    // orders the partial's stores before the counter increment.  A fence
-    // here would write back and invalidate the whole L2 in every workgroup.
-    float* mine = reinterpret_cast<float*>(ws_part + ((size_t)tile * S + split) * 64 + lane);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) __hip_atomic_store(mine + v, sum[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Partials move with 16-byte sc1 (device-coherent) buffer accesses and
+    // the counter with a device-scope atomic; the vmcnt(0) wait orders this
+    // lane's partial before the increment.  A fence here would write back
+    // and invalidate the whole L2 in every workgroup.
+    coherent_store16(ws_part, (uint32_t)((((size_t)tile * S + split) * 64 + lane) * 16),
+                     __builtin_bit_cast(uint4_t, sum));
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     uint32_t prev = 0;
@@ -440,14 +446,9 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>())) void gemv_flat_kernel
     prev = __builtin_amdgcn_readfirstlane(prev);
     if (prev != (uint32_t)(S - 1)) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    const float* all = reinterpret_cast<const float*>(ws_part + (size_t)tile * S * 64 + lane);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) sum[v] = __hip_atomic_load(all + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int s2 = 1; s2 < S; ++s2) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        sum[v] += __hip_atomic_load(all + s2 * 256 + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    const uint32_t base = (uint32_t)(((size_t)tile * S * 64 + lane) * 16);
+    sum = __builtin_bit_cast(float4_t, coherent_load16(ws_part, base));
+    for (int s2 = 1; s2 < S; ++s2) sum += __builtin_bit_cast(float4_t, coherent_load16(ws_part, base + s2 * 1024));
     if (lane == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (has_x) {

@@ -81,3 +81,270 @@ def int8_weight_only_linear(inputs: Tensor, weights: Mapping[str, Tensor], weigh
         else:
             y = _native.w8a16_linear(x, qweight, scale16)
     return y.reshape(*inputs.shape[:-1], n)
+
+
+# ============================================================================
+# Qwen3 forward over the quantized linears (quantized_model.py:124-338)
+# ============================================================================
+
+import weakref  # noqa: E402
+
+import torch.nn.functional as F  # noqa: E402
+
+from .attention import cached_scaled_dot_product_attention  # noqa: E402
+from .cache import KVCache, ResidentKVCache  # noqa: E402
+from .functional import rms_norm  # noqa: E402
+from .layers import RotaryEmbedding, apply_rotary_pos_emb  # noqa: E402
+
+QKV_FUSED = 'self_attn.qkv_proj.weight'
+GATE_UP_FUSED = 'mlp.gate_up_proj.weight'
+
+
+@dataclass
+class CausalLMOutput:
+    logits: Tensor
+    cache: object | None = None
+
+
+def _has_prepared(weights: Mapping, name: str) -> bool:
+    return name.removesuffix('.weight') + '._prepared' in weights
+
+
+def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str, Tensor], config: object,
+                                    layer_idx: int, cos: Tensor, sin: Tensor, scratch: Tensor, *,
+                                    cache: KVCache | None = None, stats: QuantizedComputeStats | None = None,
+                                    linear_backend: object | None = None) -> Tensor:
+    """One Qwen3 decoder layer (``quantized_model.py:124-228``).
+
+    Same operation order and signature as the reference; when the backend
+    prepared fused QKV / gate_up weights (``fuse_projections``) the three and
+    the two projections run as one linear each, and ``silu(gate) * up`` runs
+    as one HIP kernel.
+    """
+    def linear(inputs, name):
+        if linear_backend is not None:
+            return linear_backend.linear(inputs, weights, name)
+        return int8_weight_only_linear(inputs, weights, name, scratch, stats=stats)
+
+    eps = config.rms_norm_eps
+    hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
+    residual = hidden_states
+    states = rms_norm(hidden_states, weights['input_layernorm.weight'], eps)
+    batch_size, query_length, _ = states.shape
+    if linear_backend is not None and _has_prepared(weights, QKV_FUSED):
+        qkv = linear(states, QKV_FUSED)
+        query, key, value = qkv.split((hq * d, hkv * d, hkv * d), dim=-1)
+    else:
+        query = linear(states, 'self_attn.q_proj.weight')
+        key = linear(states, 'self_attn.k_proj.weight')
+        value = linear(states, 'self_attn.v_proj.weight')
+    query = query.reshape(batch_size, query_length, hq, d)
+    key = key.reshape(batch_size, query_length, hkv, d)
+    value = value.reshape(batch_size, query_length, hkv, d)
+    query = rms_norm(query, weights['self_attn.q_norm.weight'], eps).transpose(1, 2)
+    key = rms_norm(key, weights['self_attn.k_norm.weight'], eps).transpose(1, 2)
+    value = value.transpose(1, 2)
+    query, key = apply_rotary_pos_emb(query, key, cos, sin)
+    attention_output = cached_scaled_dot_product_attention(query, key, value, layer_idx=layer_idx, cache=cache,
+                                                           attention_mask=None, dropout_p=0.0)
+    attention_output = attention_output.transpose(1, 2).contiguous().view(batch_size, query_length, hq * d)
+    attention_output = linear(attention_output, 'self_attn.o_proj.weight')
+    hidden_states = residual + attention_output
+
+    residual = hidden_states
+    states = rms_norm(hidden_states, weights['post_attention_layernorm.weight'], eps)
+    if linear_backend is not None and _has_prepared(weights, GATE_UP_FUSED):
+        activated = _native.silu_mul(linear(states, GATE_UP_FUSED).contiguous())
+    else:
+        gate = linear(states, 'mlp.gate_proj.weight')
+        up = linear(states, 'mlp.up_proj.weight')
+        activated = F.silu(gate) * up
+    mlp_output = linear(activated, 'mlp.down_proj.weight')
+    return residual + mlp_output
+
+
+class DecodeStepGraph:
+    """One batch-1 decode token of the whole model, captured once as a HIP
+    graph over model-owned buffers: embedding row -> 40 x [add+RMSNorm, fused
+    QKV linear, attention (q/k norm, RoPE, KV append, GQA softmax), o linear,
+    add+RMSNorm, fused gate_up linear, SiLU*up, down linear] -> final norm ->
+    fp16 LM head.  Inputs are the token id and the position (device
+    scalars); every launch is a HIP kernel of this library except the
+    embedding gather and the fp16 LM-head GEMM (torch)."""
+
+    def __init__(self, model: 'QuantizedQwen3ForCausalLM', key_cache: list[Tensor], value_cache: list[Tensor],
+                 max_seq_len: int):
+        cfg, dev = model.config, model.device
+        self.model = model
+        self.max_seq_len = max_seq_len
+        self.kc = [t[0] for t in key_cache]       # [kv_heads, max_seq, head_dim] views (batch 0)
+        self.vc = [t[0] for t in value_cache]
+        self.cos, self.sin = model.rotary_emb.table(max_seq_len, dev)
+        hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        hidden = cfg.hidden_size
+        f16 = dict(dtype=torch.float16, device=dev)
+        self.token = torch.zeros(1, dtype=torch.long, device=dev)
+        self.position = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.hidden = torch.empty(1, hidden, **f16)
+        self.states = torch.empty(1, hidden, **f16)
+        self.qkv = torch.empty(1, (hq + 2 * hkv) * d, **f16)
+        self.attn = torch.empty(hq * d, **f16)
+        self.delta = torch.empty(1, hidden, **f16)
+        self.gate_up = torch.empty(1, 2 * cfg.intermediate_size, **f16)
+        self.act = torch.empty(1, cfg.intermediate_size, **f16)
+        self.logits = torch.empty(1, cfg.vocab_size, **f16)
+        self.attn_ws = torch.zeros(max(_native.decode_attention_workspace_size(hq, hkv, d, max_seq_len), 1),
+                                   dtype=torch.uint8, device=dev)
+        self.scale = 1.0 / float(d) ** 0.5
+        self.layers = [model.runtime.weights_for(i) for i in range(cfg.num_hidden_layers)]
+        calls = (model.linear_backend.calls, model.linear_backend.gemm_calls)
+        for w in self.layers:
+            for name in (QKV_FUSED, 'self_attn.o_proj.weight', GATE_UP_FUSED, 'mlp.down_proj.weight'):
+                if not _has_prepared(w, name):
+                    raise ValueError(f'decode graph needs prepared {name}')
+        self.embed = model.device_embedding()
+        self.lm_head_t = model.lm_head.t()
+        # One eager step loads every code object and the GEMM's handles, then
+        # the capture (the eager step's KV row 0 is rewritten by any prefill).
+        self._step()
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        torch.cuda.synchronize(dev)
+        model.linear_backend.calls, model.linear_backend.gemm_calls = calls   # set-up launches are not calls
+
+    def _linear(self, x: Tensor, weights: Mapping, name: str, out: Tensor) -> None:
+        prepared = weights[name.removesuffix('.weight') + '._prepared']
+        self.model.linear_backend._fused(x, prepared, out)
+
+    def _step(self) -> None:
+        cfg = self.model.config
+        eps = cfg.rms_norm_eps
+        torch.index_select(self.embed, 0, self.token, out=self.hidden)
+        for idx, w in enumerate(self.layers):
+            _native.add_rmsnorm(self.hidden, w['input_layernorm.weight'], eps, delta=None if idx == 0 else self.delta,
+                                out=self.states, out_sum=self.hidden)
+            self._linear(self.states, w, QKV_FUSED, self.qkv)
+            _native.decode_attention(self.qkv.view(-1), cfg.num_attention_heads, cfg.num_key_value_heads,
+                                     w['self_attn.q_norm.weight'], w['self_attn.k_norm.weight'], eps, self.cos,
+                                     self.sin, self.position, self.kc[idx], self.vc[idx], self.scale, out=self.attn,
+                                     workspace=self.attn_ws)
+            self._linear(self.attn.view(1, -1), w, 'self_attn.o_proj.weight', self.delta)
+            _native.add_rmsnorm(self.hidden, w['post_attention_layernorm.weight'], eps, delta=self.delta,
+                                out=self.states, out_sum=self.hidden)
+            self._linear(self.states, w, GATE_UP_FUSED, self.gate_up)
+            _native.silu_mul(self.gate_up, out=self.act)
+            self._linear(self.act, w, 'mlp.down_proj.weight', self.delta)
+        _native.add_rmsnorm(self.hidden, self.model.final_norm, eps, delta=self.delta, out=self.states)
+        torch.mm(self.states, self.lm_head_t, out=self.logits)
+
+    def run(self, token: Tensor, position: int) -> Tensor:
+        if not 0 <= position < self.max_seq_len:
+            raise ValueError(f'KV cache capacity exceeded: requested {position + 1}, capacity {self.max_seq_len}')
+        self.token.copy_(token.reshape(1), non_blocking=True)
+        self.position.fill_(position)
+        self.graph.replay()
+        backend = self.model.linear_backend
+        backend.calls += 4 * len(self.layers)       # fused QKV, o, fused gate_up, down per layer
+        backend.gemm_calls += 4 * len(self.layers)
+        return self.logits
+
+
+class QuantizedQwen3ForCausalLM:
+    """Qwen3 over the quantized decoder (``quantized_model.py:231-338``).
+
+    ``store``/``runtime``/``linear_backend`` as in the reference.  Prefill and
+    multi-token calls run eagerly layer by layer; single-token calls with a
+    cache from ``make_resident_cache`` (batch 1) replay a captured
+    ``DecodeStepGraph`` bound to that cache's storage.
+    """
+
+    def __init__(self, store, runtime, *, device: str | torch.device, profile_compute: bool = False,
+                 linear_backend: object | None = None, decode_graph: bool = True) -> None:
+        self.store = store
+        self.runtime = runtime
+        self.config = store.config
+        self.device = torch.device(device)
+        self.dtype = store.compute_dtype
+        self.final_norm = store.final_norm.to(self.device)
+        self.lm_head = store.lm_head.to(self.device)
+        self.rotary_emb = RotaryEmbedding(self.config.head_dim, self.config.rope_theta).to(self.device)
+        self.linear_backend = linear_backend
+        self.dequant_scratch = torch.empty(store.max_dequant_elements if linear_backend is None else 0,
+                                           device=self.device, dtype=self.dtype)
+        self.compute_stats = QuantizedComputeStats(enabled=profile_compute)
+        self.decode_graph_enabled = decode_graph and linear_backend is not None and \
+            hasattr(linear_backend, 'fuse_projections')
+        if linear_backend is not None and hasattr(linear_backend, 'fuse_projections'):
+            for idx in range(self.config.num_hidden_layers):
+                linear_backend.fuse_projections(runtime.weights_for(idx))
+        self._embed_device = None
+        self._kv_pool: dict = {}
+
+    def device_embedding(self) -> Tensor:
+        if self._embed_device is None:
+            self._embed_device = self.store.embed_tokens.to(self.device)
+        return self._embed_device
+
+    def make_resident_cache(self, *, batch_size: int, max_seq_len: int,
+                            device: str | torch.device | None = None) -> ResidentKVCache:
+        """A fresh cache (lengths 0).  Its storage comes from a model-owned
+        pool: a cache of the same shape whose previous owner object is gone
+        is reused together with the decode graph captured for it, so repeated
+        generations capture once; caches alive at the same time never share
+        storage."""
+        dev = torch.device(device or self.device)
+        cfg = self.config
+        cache = ResidentKVCache(num_layers=0, batch_size=batch_size, num_key_value_heads=cfg.num_key_value_heads,
+                                max_seq_len=max_seq_len, head_dim=cfg.head_dim, device=dev, dtype=self.dtype)
+        entries = self._kv_pool.setdefault((batch_size, max_seq_len, str(dev)), [])
+        entry = next((e for e in entries if e['owner']() is None), None)
+        if entry is None:
+            shape = (batch_size, cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
+            entry = {'k': [torch.zeros(shape, device=dev, dtype=self.dtype) for _ in range(cfg.num_hidden_layers)],
+                     'v': [torch.zeros(shape, device=dev, dtype=self.dtype) for _ in range(cfg.num_hidden_layers)],
+                     'graph': None}
+            if self.decode_graph_enabled and batch_size == 1 and dev.type == 'cuda':
+                entry['graph'] = DecodeStepGraph(self, entry['k'], entry['v'], max_seq_len)
+            entries.append(entry)
+        entry['owner'] = weakref.ref(cache)
+        cache.key_cache, cache.value_cache = entry['k'], entry['v']
+        cache.lengths = [0] * cfg.num_hidden_layers
+        cache._decode_graph = entry['graph']
+        return cache
+
+    @torch.inference_mode()
+    def __call__(self, input_ids: Tensor, *, cache: KVCache | None = None, position_ids: Tensor | None = None,
+                 logits_to_keep: int = 0, **_: object) -> CausalLMOutput:
+        graph = getattr(cache, '_decode_graph', None)
+        if graph is not None and position_ids is None and input_ids.shape == (1, 1):
+            past = cache.get_seq_length(0)
+            if any(n != past for n in cache.lengths):
+                raise RuntimeError('decode graph needs every layer of the cache at the same length')
+            logits = graph.run(input_ids.to(self.device), past)
+            cache.lengths[:] = [past + 1] * len(cache.lengths)
+            return CausalLMOutput(logits=logits.view(1, 1, -1).clone(), cache=cache)
+
+        ids_cpu = input_ids.detach().to(device='cpu')
+        hidden_cpu = F.embedding(ids_cpu, self.store.embed_tokens)
+        hidden_states = hidden_cpu.to(self.device)
+        past_length = cache.get_seq_length(0) if cache is not None else 0
+        query_length = input_ids.shape[1]
+        if position_ids is None:
+            position_ids = torch.arange(past_length, past_length + query_length,
+                                        device=self.device).expand(input_ids.shape[0], -1)
+        cos, sin = self.rotary_emb(hidden_states, position_ids)
+        self.runtime.begin_forward()
+        for layer_idx in range(self.config.num_hidden_layers):
+            weights = self.runtime.weights_for(layer_idx)
+            hidden_states = quantized_decoder_layer_forward(
+                hidden_states, weights, self.config, layer_idx, cos, sin, self.dequant_scratch, cache=cache,
+                stats=self.compute_stats, linear_backend=self.linear_backend)
+            self.runtime.after_layer(layer_idx)
+        self.runtime.end_forward()
+        hidden_states = rms_norm(hidden_states, self.final_norm, self.config.rms_norm_eps)
+        if logits_to_keep > 0:
+            hidden_states = hidden_states[:, -logits_to_keep:, :]
+        logits = F.linear(hidden_states, self.lm_head)
+        return CausalLMOutput(logits=logits, cache=cache)

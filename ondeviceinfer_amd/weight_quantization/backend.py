@@ -75,6 +75,13 @@ def decode_weight(weights: dict, name: str, *, group_size: int = 128) -> torch.T
                              n, k, group_size)
 
 
+# fused linear -> the prepared projections it concatenates along N, in order
+FUSED_PROJECTIONS = {
+    'self_attn.qkv_proj': ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj'),
+    'mlp.gate_up_proj': ('mlp.gate_proj', 'mlp.up_proj'),
+}
+
+
 class PreparedW4(NamedTuple):
     """What ``prepare`` stores under ``prefix._prepared`` for the W4A16 path."""
     tiles: torch.Tensor       # uint8, gfx950 tile layout
@@ -303,6 +310,45 @@ class CompressedLinearBackend:
             n, k = q.shape
             scale = layer[prefix + '.weight_scale'].reshape(-1).half().contiguous()
             layer[prefix + '._prepared'] = PreparedW8(q.contiguous(), scale, k, n)
+
+    def fuse_projections(self, layer: dict) -> None:
+        """Add ``self_attn.qkv_proj._prepared`` and ``mlp.gate_up_proj._prepared``:
+        the prepared q/k/v (gate/up) weights concatenated along N, so each
+        group runs as one linear whose output is ``[q | k | v]``
+        (``[gate | up]``).  W4 tiles and meta are tile-major and INT8 rows are
+        row-major, so concatenation is a plain copy; afterwards the parts'
+        own ``_prepared`` entries are views into the fused buffers (no
+        duplicate weights).  Layers whose parts do not line up (mixed formats,
+        N not a multiple of 16) are left as they are."""
+        for fused, parts in FUSED_PROJECTIONS.items():
+            preps = [layer.get(p + '._prepared') for p in parts]
+            if fused + '._prepared' in layer or any(p is None for p in preps):
+                continue
+            if all(isinstance(p, PreparedW4) for p in preps):
+                if len({(p.k, p.group_size) for p in preps}) != 1 or any(p.n % 16 for p in preps):
+                    continue
+                tiles = torch.cat([p.tiles for p in preps])
+                meta = torch.cat([p.meta for p in preps])
+                n, k, g = sum(p.n for p in preps), preps[0].k, preps[0].group_size
+                ws_bytes = _native.w4a16_workspace_size(1, n, k, g)
+                ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=tiles.device) if ws_bytes else None
+                layer[fused + '._prepared'] = PreparedW4(tiles, meta, ws, k, n, g)
+                t0 = m0 = 0
+                for part, p in zip(parts, preps):
+                    layer[part + '._prepared'] = p._replace(tiles=tiles[t0:t0 + p.tiles.numel()],
+                                                            meta=meta[m0:m0 + p.meta.numel()])
+                    t0 += p.tiles.numel()
+                    m0 += p.meta.numel()
+            elif all(isinstance(p, PreparedW8) for p in preps):
+                if len({p.k for p in preps}) != 1:
+                    continue
+                q = torch.cat([p.qweight for p in preps])
+                sc = torch.cat([p.scale for p in preps])
+                layer[fused + '._prepared'] = PreparedW8(q, sc, preps[0].k, int(q.shape[0]))
+                r0 = 0
+                for part, p in zip(parts, preps):
+                    layer[part + '._prepared'] = PreparedW8(q[r0:r0 + p.n], sc[r0:r0 + p.n], p.k, p.n)
+                    r0 += p.n
 
     def linear(self, inputs: torch.Tensor, weights: dict, name: str) -> torch.Tensor:
         self.calls += 1

@@ -1,0 +1,133 @@
+"""Random Qwen3-shaped compressed-tensors models and a checkpoint writer.
+
+There is no real checkpoint or network on the benchmark machines, so the
+end-to-end benchmark and the loader tests need pack-quantized weights of the
+right shapes.  ``random_compressed_store`` draws them directly in the
+compressed-tensors layout that ``load_compressed_store`` validates
+(``ondeviceinfer/weight_quantization/backend.py:69-128``): per linear
+``weight_packed`` int32 ``[n, k/8]`` (random codes), ``weight_scale`` fp16
+``[n, k/G]`` (positive), ``weight_zero_point`` int32 ``[n/8, k/G]`` (random
+codes; omitted for symmetric uint4b8), ``weight_shape``; fp16 norms near 1;
+fp16 embedding and LM head on the host, as the reference keeps them.
+
+``write_compressed_checkpoint`` writes such a store as safetensors shards +
+``model.safetensors.index.json`` + ``config.json`` with a
+``quantization_config`` of format ``pack-quantized`` (the on-disk contract of
+``calibrate_weight_quant.py:97-102,150`` in the reference).
+"""
+from __future__ import annotations
+
+import json
+from dataclasses import asdict
+from pathlib import Path
+
+import torch
+
+from ..config import Qwen3Config
+from ..runtime.quantized import LINEAR_WEIGHT_NAMES, NORM_WEIGHT_NAMES
+from .backend import CompressedStore
+
+
+def linear_shapes(cfg: Qwen3Config) -> dict[str, tuple[int, int]]:
+    """``name -> (n, k)`` of the seven decoder linears."""
+    hidden, inter = cfg.hidden_size, cfg.intermediate_size
+    kv = cfg.num_key_value_heads * cfg.head_dim
+    q = cfg.num_attention_heads * cfg.head_dim
+    return {
+        'self_attn.q_proj.weight': (q, hidden), 'self_attn.k_proj.weight': (kv, hidden),
+        'self_attn.v_proj.weight': (kv, hidden), 'self_attn.o_proj.weight': (hidden, q),
+        'mlp.gate_proj.weight': (inter, hidden), 'mlp.up_proj.weight': (inter, hidden),
+        'mlp.down_proj.weight': (hidden, inter),
+    }
+
+
+def random_compressed_store(cfg: Qwen3Config, *, seed: int = 0, device: str | torch.device = 'cpu',
+                            group_size: int = 128, symmetric: bool = False,
+                            scale_range: tuple[float, float] = (0.0005, 0.0025)) -> CompressedStore:
+    """A random W4 (G=``group_size``) Qwen3 model; decoder tensors on ``device``,
+    embedding / final norm / LM head on the host."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cpu_gen = torch.Generator().manual_seed(seed + 1)
+    lo, hi = scale_range
+    layers = []
+    for _ in range(cfg.num_hidden_layers):
+        layer = {}
+        for name, (n, k) in linear_shapes(cfg).items():
+            prefix = name.removesuffix('.weight')
+            layer[prefix + '.weight_packed'] = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32,
+                                                             device=device, generator=gen)
+            layer[prefix + '.weight_scale'] = (torch.rand((n, k // group_size), device=device, generator=gen)
+                                               * (hi - lo) + lo).half()
+            if not symmetric:
+                layer[prefix + '.weight_zero_point'] = torch.randint(-2**31, 2**31 - 1, (n // 8, k // group_size),
+                                                                     dtype=torch.int32, device=device, generator=gen)
+            layer[prefix + '.weight_shape'] = torch.tensor([n, k], dtype=torch.int64)
+        for name in NORM_WEIGHT_NAMES:
+            size = cfg.head_dim if 'q_norm' in name or 'k_norm' in name else cfg.hidden_size
+            layer[name] = (1.0 + 0.1 * torch.randn(size, device=device, generator=gen)).half()
+        layers.append(layer)
+    embed = (torch.randn(cfg.vocab_size, cfg.hidden_size, generator=cpu_gen) * 0.02).half()
+    lm_head = embed if cfg.tie_word_embeddings else \
+        (torch.randn(cfg.vocab_size, cfg.hidden_size, generator=cpu_gen) * 0.02).half()
+    final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden_size, generator=cpu_gen)).half()
+    manifest = {'source': 'synthetic', 'seed': seed, 'quantization_config': quantization_config(group_size, symmetric)}
+    return CompressedStore(cfg, layers, embed, final_norm, lm_head, manifest)
+
+
+def quantization_config(group_size: int, symmetric: bool) -> dict:
+    """compressed-tensors ``quantization_config`` for W4A16 pack-quantized."""
+    return {
+        'quant_method': 'compressed-tensors', 'format': 'pack-quantized',
+        'config_groups': {'group_0': {
+            'targets': ['Linear'],
+            'weights': {'num_bits': 4, 'type': 'int', 'symmetric': symmetric, 'strategy': 'group',
+                        'group_size': group_size, 'actorder': None, 'dynamic': False},
+            'input_activations': None}},
+        'ignore': ['lm_head'],
+    }
+
+
+def config_json(cfg: Qwen3Config) -> dict:
+    raw = asdict(cfg)
+    raw['model_type'] = 'qwen3'
+    raw['architectures'] = ['Qwen3ForCausalLM']
+    raw['torch_dtype'] = 'float16'
+    return raw
+
+
+def write_compressed_checkpoint(path: str | Path, store: CompressedStore, *, layers_per_shard: int = 8) -> Path:
+    """Write ``store`` as a compressed-tensors checkpoint that
+    ``load_compressed_store`` reads back tensor for tensor."""
+    from safetensors.torch import save_file
+    path = Path(path)
+    path.mkdir(parents=True, exist_ok=True)
+    weight_map: dict[str, str] = {}
+    n_layers = len(store.layers)
+    shards = [list(range(i, min(i + layers_per_shard, n_layers))) for i in range(0, n_layers, layers_per_shard)]
+    total = len(shards) + 1
+    for s_idx, layer_ids in enumerate(shards):
+        fname = f'model-{s_idx + 1:05d}-of-{total:05d}.safetensors'
+        tensors = {}
+        for li in layer_ids:
+            for key, value in store.layers[li].items():
+                if isinstance(value, torch.Tensor):
+                    tensors[f'model.layers.{li}.{key}'] = value.detach().to('cpu').contiguous()
+        save_file(tensors, str(path / fname))
+        weight_map.update({name: fname for name in tensors})
+    fname = f'model-{total:05d}-of-{total:05d}.safetensors'
+    tensors = {'model.embed_tokens.weight': store.embed_tokens.cpu().contiguous(),
+               'model.norm.weight': store.final_norm.cpu().contiguous()}
+    if not store.config.tie_word_embeddings:
+        tensors['lm_head.weight'] = store.lm_head.cpu().contiguous()
+    save_file(tensors, str(path / fname))
+    weight_map.update({name: fname for name in tensors})
+    (path / 'model.safetensors.index.json').write_text(json.dumps({'metadata': {}, 'weight_map': weight_map}, indent=1))
+    raw = config_json(store.config)
+    raw['quantization_config'] = store.manifest.get('quantization_config') or quantization_config(128, False)
+    (path / 'config.json').write_text(json.dumps(raw, indent=1))
+    return path
+
+
+__all__ = ['linear_shapes', 'random_compressed_store', 'quantization_config', 'write_compressed_checkpoint',
+           'LINEAR_WEIGHT_NAMES']

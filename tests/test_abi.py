@@ -8,12 +8,15 @@ import pytest
 
 from ondeviceinfer_amd import _native
 
-HEADER = Path(__file__).resolve().parents[1] / 'include' / 'ondeviceinfer_wq.h'
+HEADERS = sorted((Path(__file__).resolve().parents[1] / 'include').glob('*.h'))
 
 
 def declared_functions() -> list[str]:
-    text = re.sub(r'/\*.*?\*/', '', HEADER.read_text(), flags=re.S)
-    return re.findall(r'^\s*(?:const\s+char\s*\*|int)\s+(wq_\w+)\s*\(', text, flags=re.M)
+    names = []
+    for header in HEADERS:
+        text = re.sub(r'/\*.*?\*/', '', header.read_text(), flags=re.S)
+        names += re.findall(r'^\s*(?:const\s+char\s*\*|int)\s+(wq_\w+)\s*\(', text, flags=re.M)
+    return names
 
 
 def test_header_declares_the_bound_entry_points():

@@ -1,0 +1,194 @@
+"""Decode-step operators on the GPU against the oracle (oracle/qwen3.py):
+add + RMSNorm, SiLU * up, and the fused q/k-norm + RoPE + KV-append + GQA
+attention kernel, through the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qdq, qwen3
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope='module')
+def nat(gpu):
+    from ondeviceinfer_amd import _native
+    _native.load()
+    return _native
+
+
+def _close(got, ref, rel=4e-3):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref).max()
+    assert err <= rel * max(np.abs(ref).max(), 1e-3), (err, np.abs(ref).max())
+
+
+@pytest.mark.parametrize('rows,n,with_delta,in_place', [(1, 5120, True, True), (1, 5120, False, False),
+                                                        (37, 512, True, False), (4096, 5120, True, True)])
+def test_add_rmsnorm(nat, rows, n, with_delta, in_place):
+    print(f'[add_rmsnorm] rows={rows} n={n} delta={with_delta} in_place={in_place}', flush=True)
+    rng = np.random.default_rng(rows + n)
+    x = (rng.standard_normal((rows, n)) * 3).astype(np.float16)
+    d = (rng.standard_normal((rows, n)) * 2).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float16)
+    tx, td, tw = (torch.from_numpy(a).cuda() for a in (x, d, w))
+    out_sum = tx if in_place else torch.empty_like(tx)
+    y = nat.add_rmsnorm(tx, tw, 1e-6, delta=td if with_delta else None, out_sum=out_sum)
+    torch.cuda.synchronize()
+    s = (x + d).astype(np.float16) if with_delta else x
+    assert np.array_equal(out_sum.cpu().numpy(), s)
+    _close(y.cpu().numpy(), qwen3.rms_norm(s, w, 1e-6))
+
+
+def test_silu_mul(nat):
+    rng = np.random.default_rng(5)
+    gu = (rng.standard_normal((3, 2 * 17408)) * 3).astype(np.float16)
+    y = nat.silu_mul(torch.from_numpy(gu).cuda()).cpu().numpy()
+    ref = qwen3.swiglu(gu[:, :17408], gu[:, 17408:])
+    ulp = np.abs(y.astype(np.float64) - ref.astype(np.float64)) / np.maximum(np.abs(ref.astype(np.float64)), 2 ** -14)
+    assert ulp.max() <= 2 ** -9
+
+
+class AttnCase:
+    """Random qkv and cache rows 0..pos-1; rows past pos hold NaN so a read
+    beyond the attended range would poison the output."""
+
+    def __init__(self, h, kv, max_seq, seed, norms=True):
+        self.h, self.kv, self.max_seq = h, kv, max_seq
+        rng = np.random.default_rng(seed)
+        self.rng = rng
+        self.qn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float16) if norms else None
+        self.kn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float16) if norms else None
+        self.cos, self.sin = qwen3.rotary_tables(128, 1_000_000.0, np.arange(max_seq))
+        self.kc = np.full((kv, max_seq, 128), np.nan, dtype=np.float16)
+        self.vc = np.full((kv, max_seq, 128), np.nan, dtype=np.float16)
+
+    def fill(self, upto):
+        self.kc[:, :upto] = self.rng.standard_normal((self.kv, upto, 128)).astype(np.float16)
+        self.vc[:, :upto] = self.rng.standard_normal((self.kv, upto, 128)).astype(np.float16)
+
+    def qkv(self):
+        return (self.rng.standard_normal((self.h + 2 * self.kv) * 128) * 2).astype(np.float16)
+
+    def expected(self, qkv, pos):
+        h, kv = self.h, self.kv
+        q = qkv[:h * 128].reshape(h, 1, 128)
+        k = qkv[h * 128:(h + kv) * 128].reshape(kv, 1, 128)
+        v = qkv[(h + kv) * 128:].reshape(kv, 1, 128)
+        if self.qn is not None:
+            q = qwen3.rms_norm(q, self.qn, 1e-6)
+            k = qwen3.rms_norm(k, self.kn, 1e-6)
+        c, s = self.cos[pos:pos + 1], self.sin[pos:pos + 1]
+        q, k = qwen3.apply_rope(q, c, s), qwen3.apply_rope(k, c, s)
+        keys = np.concatenate([self.kc[:, :pos], k], axis=1)
+        vals = np.concatenate([self.vc[:, :pos], v], axis=1)
+        return qwen3.attention(q, keys, vals, None).reshape(-1), k[:, 0], v[:, 0]
+
+    def tensors(self):
+        t = {'kc': torch.from_numpy(self.kc).cuda(), 'vc': torch.from_numpy(self.vc).cuda(),
+             'cos': torch.from_numpy(self.cos).cuda(), 'sin': torch.from_numpy(self.sin).cuda()}
+        t['qn'] = None if self.qn is None else torch.from_numpy(self.qn).cuda()
+        t['kn'] = None if self.kn is None else torch.from_numpy(self.kn).cuda()
+        return t
+
+
+def _run(nat, case, t, qkv, pos, ws):
+    p = torch.tensor([pos], dtype=torch.int32, device='cuda')
+    out = nat.decode_attention(torch.from_numpy(qkv).cuda(), case.h, case.kv, t['qn'], t['kn'], 1e-6, t['cos'],
+                               t['sin'], p, t['kc'], t['vc'], 1.0 / np.sqrt(128.0), workspace=ws)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize('h,kv,max_seq,positions', [
+    (40, 8, 4224, (0, 1, 63, 64, 65, 1000, 4223)),   # Qwen3-14B geometry at a 4K+128 cache
+    (40, 8, 64, (0, 10, 63)),                         # one chunk: no cross-workgroup merge
+    (64, 8, 300, (0, 129, 299)),                      # 8 query heads per kv head
+    (8, 8, 200, (5, 199)),                            # no grouping
+])
+def test_decode_attention_matches_oracle(nat, h, kv, max_seq, positions):
+    case = AttnCase(h, kv, max_seq, seed=h + max_seq)
+    ws = torch.zeros(max(nat.decode_attention_workspace_size(h, kv, 128, max_seq), 1), dtype=torch.uint8,
+                     device='cuda')
+    for pos in positions:
+        print(f'[decode_attention] h={h} kv={kv} max_seq={max_seq} pos={pos}', flush=True)
+        case.kc[:] = np.nan
+        case.vc[:] = np.nan
+        case.fill(pos)
+        t = case.tensors()
+        qkv = case.qkv()
+        got = _run(nat, case, t, qkv, pos, ws)
+        ref, k_new, v_new = case.expected(qkv, pos)
+        m = qdq.parity_metrics(got, ref)
+        assert qdq.parity_ok(m), (pos, m)
+        kc = t['kc'].cpu().numpy()
+        assert np.array_equal(t['vc'].cpu().numpy()[:, pos], v_new)
+        _close(kc[:, pos], k_new)
+        assert np.isnan(kc[:, pos + 1:]).all() and np.array_equal(kc[:, :pos], case.kc[:, :pos])
+    if ws.numel() >= 256:
+        assert int(ws[:256].view(torch.int32).abs().sum()) == 0     # counters re-armed
+
+
+def test_decode_attention_without_norms(nat):
+    case = AttnCase(16, 4, 500, seed=9, norms=False)
+    ws = torch.zeros(nat.decode_attention_workspace_size(16, 4, 128, 500), dtype=torch.uint8, device='cuda')
+    case.fill(321)
+    t = case.tensors()
+    qkv = case.qkv()
+    got = _run(nat, case, t, qkv, 321, ws)
+    ref, _, _ = case.expected(qkv, 321)
+    assert qdq.parity_ok(qdq.parity_metrics(got, ref))
+
+
+def test_decode_attention_out_of_range_position_leaves_cache(nat):
+    case = AttnCase(16, 4, 128, seed=3)
+    case.fill(128)
+    t = case.tensors()
+    before = t['kc'].clone()
+    ws = torch.zeros(nat.decode_attention_workspace_size(16, 4, 128, 128), dtype=torch.uint8, device='cuda')
+    got = _run(nat, case, t, case.qkv(), 128, ws)
+    assert np.isnan(got).all()
+    assert torch.equal(t['kc'], before)
+    # the next in-range call still works with the same workspace
+    qkv = case.qkv()
+    case.kc = t['kc'].cpu().numpy()
+    got = _run(nat, case, t, qkv, 100, ws)
+    ref, _, _ = case.expected(qkv, 100)
+    assert qdq.parity_ok(qdq.parity_metrics(got, ref))
+
+
+def test_decode_attention_graph_replays_follow_the_position(nat):
+    """Captured once, replayed for consecutive positions (each replay appends
+    one row), with eager work and synchronizations between replays."""
+    case = AttnCase(40, 8, 1024, seed=11)
+    case.fill(500)
+    t = case.tensors()
+    ws = torch.zeros(nat.decode_attention_workspace_size(40, 8, 128, 1024), dtype=torch.uint8, device='cuda')
+    pos_t = torch.zeros(1, dtype=torch.int32, device='cuda')
+    qkv_t = torch.empty((40 + 16) * 128, dtype=torch.float16, device='cuda')
+    out_t = torch.empty(40 * 128, dtype=torch.float16, device='cuda')
+
+    def step():
+        nat.decode_attention(qkv_t, 40, 8, t['qn'], t['kn'], 1e-6, t['cos'], t['sin'], pos_t, t['kc'], t['vc'],
+                             1.0 / np.sqrt(128.0), out=out_t, workspace=ws)
+
+    qkv_t.copy_(torch.from_numpy(case.qkv()))
+    pos_t.fill_(999)
+    step()                                          # eager warm-up (row 999 is not attended below)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for pos in range(500, 504):
+        qkv = case.qkv()
+        qkv_t.copy_(torch.from_numpy(qkv))
+        pos_t.fill_(pos)
+        g.replay()
+        torch.cuda.synchronize()
+        ref, k_new, v_new = case.expected(qkv, pos)
+        assert qdq.parity_ok(qdq.parity_metrics(out_t.cpu().numpy(), ref)), pos
+        case.kc[:, pos] = t['kc'][:, pos].cpu().numpy()
+        case.vc[:, pos] = v_new
+        _ = torch.randn(1000, device='cuda').sum().item()   # eager work between replays
