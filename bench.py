@@ -1,25 +1,31 @@
 #!/usr/bin/env python3
-"""Benchmark: W4A16 G=128 decode GEMV over a Qwen3-14B-shaped decoder.
+"""Benchmark: Qwen3-14B-shaped AWQ-INT4 (W4A16, G=128) decode on one MI355X.
 
-One *step* is one decode token's worth of projection GEMVs at M=1: for each of
-the 40 decoder layers, q 5120->5120, k and v 5120->1024, o 5120->5120, gate and
-up 5120->17408 and down 17408->5120 (280 launches), every layer with its own
-resident weights (6.86 GB of packed uint4 + scales + zero points), so no weight
-is served from the 256 MB Infinity Cache.  The 280 launches are captured once
-in a HIP graph and the graph is replayed per step.  Inputs are resident in HBM
-before the timed region.
+Headline (the workload the metric's published number is
+quoted on): batch 1, a 4096-token random prompt, greedy decode with the fp16
+KV cache resident, random-init weights of the Qwen3-14B architecture (40
+layers, hidden 5120, 40/8 heads of 128, SwiGLU 17408, vocab 151936), the
+decoder linears uint4 with fp16 group-128 scales and zero points.  One *step*
+is one decode token: a replay of the captured decode-step graph (40 x [add +
+RMSNorm, fused QKV GEMV, fused attention kernel, o GEMV, add + RMSNorm, fused
+gate_up GEMV, SiLU*up, down GEMV], final norm, fp16 LM head) plus the argmax.
+After the prefill and ``--warmup`` untimed steps, ``--steps`` steps are timed;
+``value`` = steps / seconds (tok/s), compared with the reference's published
+26.358 tok/s (AWQ-INT4 + Marlin, RTX 3090, same workload).
 
-``value`` = algorithmic bytes of the step / step time (GB/s).  Algorithmic
-bytes per GEMV: ``N*K/2 + N*(K/128)*2 + N*(K/128)/2 + 2*M*K + 2*M*N``.
-
-Also printed in the same JSON line:
-* ``roofline``: the dominant kernel's algorithmic bytes per launch / its
-  average launch time, measured here with HIP events around a graph of that
-  kernel's launches on the stream they run on;
-* ``prefill``: the M=4096 W4A16 GEMM (config 3) in TFLOP/s vs dense fp16 MFMA;
+Also in the same JSON line:
+* ``gemv_pass``: the 280 per-projection decode GEMVs of one token
+  (q, k, v, o, gate, up, down x 40 layers) replayed as one graph; GB/s of
+  algorithmic bytes ``N*K/2 + N*(K/128)*2.5 + 2MK + 2MN``;
+* ``roofline``: the dominant kernel of the decode step (largest time per
+  token), its algorithmic bytes per launch / its average launch time measured
+  here with HIP events around a graph of that kernel's launches on the stream
+  they run on; ``traffic`` from the committed rocprofv3 counter summary;
+* ``decode_step_kernels``: the same timing for every kernel of the step;
+* ``prefill``: the M=4096 W4A16 GEMM per shape, TFLOP/s;
 * ``copy_ceiling``: a device-to-device copy's GB/s on the same box;
-* ``cpu_baseline``: the numpy QDQ oracle (decode + fp32 GEMV) on one decoder
-  layer's seven projections, single-threaded, on this host.
+* ``cpu_baseline``: the numpy QDQ oracle on one decoder layer's decode work,
+  scaled to tok/s for the 40-layer model.
 """
 from __future__ import annotations
 
@@ -34,13 +40,20 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = 'Qwen3-14B AWQ-INT4 decode tok/s at B=1; W4A16 GEMV % of HBM peak'
+PUBLISHED_TOKS = 26.358          # AWQ INT4 G=128 + vLLM Marlin, RTX 3090, same workload
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 GROUP = 128
-HIDDEN, INTER, KV = 5120, 17408, 1024
+PROMPT = 4096
+HIDDEN, INTER, KV, QKV, GATE_UP = 5120, 17408, 1024, 7168, 34816
 LAYER_SHAPES = [  # (name, K, N) in decoder order
-    ('q_proj', HIDDEN, HIDDEN), ('k_proj', HIDDEN, KV), ('v_proj', HIDDEN, KV), ('o_proj', HIDDEN, HIDDEN),
-    ('gate_proj', HIDDEN, INTER), ('up_proj', HIDDEN, INTER), ('down_proj', INTER, HIDDEN),
+    ('self_attn.q_proj', HIDDEN, HIDDEN), ('self_attn.k_proj', HIDDEN, KV), ('self_attn.v_proj', HIDDEN, KV),
+    ('self_attn.o_proj', HIDDEN, HIDDEN), ('mlp.gate_proj', HIDDEN, INTER), ('mlp.up_proj', HIDDEN, INTER),
+    ('mlp.down_proj', INTER, HIDDEN),
+]
+STEP_LINEARS = [  # the four linears of the decode step (fused where the model fuses)
+    ('self_attn.qkv_proj', HIDDEN, QKV), ('self_attn.o_proj', HIDDEN, HIDDEN),
+    ('mlp.gate_up_proj', HIDDEN, GATE_UP), ('mlp.down_proj', INTER, HIDDEN),
 ]
 
 
@@ -50,26 +63,6 @@ def w4_bytes(m: int, n: int, k: int, g: int = GROUP) -> int:
 
 def log(msg: str) -> None:
     print(f'[bench] {msg}', file=sys.stderr, flush=True)
-
-
-def make_layer_weights(torch, native, n_layers: int, device):
-    """Random uint4 codes / fp16 scales / zero points, repacked by the HIP repack."""
-    gen = torch.Generator(device=device)
-    gen.manual_seed(0)
-    layers = []
-    for _ in range(n_layers):
-        layer = {}
-        for name, k, n in LAYER_SHAPES:
-            packed = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, device=device, generator=gen)
-            scale = (torch.rand((n, k // GROUP), device=device, generator=gen) * 0.008 + 0.002).half()
-            zero = torch.randint(-2**31, 2**31 - 1, (n // 8, k // GROUP), dtype=torch.int32, device=device,
-                                 generator=gen)
-            tiles, meta = native.w4_repack(packed, scale, zero, n, k, GROUP)
-            layer[name] = (tiles, meta, n, k)
-            del packed, scale, zero
-        layers.append(layer)
-    torch.cuda.synchronize()
-    return layers
 
 
 def time_graph(torch, graph, reps: int) -> float:
@@ -123,47 +116,71 @@ def profiled_traffic(kernel: str, shape: str):
     return None if rec is None else int(rec['hbm_bytes_per_launch'])
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """numpy QDQ oracle on one decoder layer's seven projections (one thread)."""
+def cpu_baseline(budget_s: float, layers: int) -> dict:
+    """The numpy QDQ oracle (decode_weight + fp32 GEMV, one BLAS thread) on one
+    decoder layer's decode-token work, scaled to tok/s for `layers` layers."""
     import numpy as np
     from threadpoolctl import threadpool_limits
-    from oracle import qdq, synth
+    from oracle import qdq, qwen3, synth
     cases = []
     for name, k, n in LAYER_SHAPES:
         w, x = synth.w4_case(n, k, 1, seed=0, name=f'{name}.weight')
-        cases.append((name, k, n, w, x))
-    total_bytes = sum(w4_bytes(1, n, k) for _, k, n, _, _ in cases)
+        cases.append((name, w, x))
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((40, 1, 128)).astype(np.float16)
+    kc = rng.standard_normal((8, PROMPT, 128)).astype(np.float16)
+    vc = rng.standard_normal((8, PROMPT, 128)).astype(np.float16)
     times = []
     with threadpool_limits(limits=1):
         t_begin = time.perf_counter()
         while True:
             t0 = time.perf_counter()
-            for name, _, _, w, x in cases:
+            for name, w, x in cases:
                 qdq.qdq_linear(x, w, f'{name}.weight')
+            qwen3.attention(q, kc, vc, None)
             times.append(time.perf_counter() - t0)
             if time.perf_counter() - t_begin > budget_s or len(times) >= 10:
                 break
     sec = float(np.median(times))
-    return {'value': round(total_bytes / sec / 1e9, 4), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
-            'sample': f'oracle.qdq.qdq_linear (numpy decode_weight + fp32 GEMV, 1 BLAS thread) over one '
-                      f'decoder layer\'s 7 W4A16 projections at M=1 ({total_bytes / 1e6:.1f} MB algorithmic), '
-                      f'median of {len(times)} passes = {sec:.3f} s/pass',
-            'ms_per_layer': round(sec * 1000, 3), 'host_cpu_count': os.cpu_count()}
+    per_token = sec * layers
+    return {'value': round(1.0 / per_token, 6), 'unit': 'tok/s', 'cores': 1, 'kind': 'port',
+            'sample': f'one decoder layer of the decode token on the host: oracle.qdq.qdq_linear (numpy '
+                      f'decode_weight + fp32 GEMV) over the 7 W4A16 projections at M=1 plus oracle.qwen3.attention '
+                      f'over a {PROMPT}-row KV cache, 1 BLAS thread, median of {len(times)} passes = {sec:.3f} s; '
+                      f'x {layers} layers (LM head, norms and RoPE not included)',
+            'seconds_per_layer': round(sec, 3), 'host_cpu_count': os.cpu_count()}
+
+
+def build_model(torch, layers: int, device):
+    from ondeviceinfer_amd.config import QWEN3_14B, Qwen3Config
+    from ondeviceinfer_amd.quantized_model import QuantizedQwen3ForCausalLM
+    from ondeviceinfer_amd.weight_quantization.backend import CompressedLinearBackend, CompressedResidentRuntime
+    from ondeviceinfer_amd.weight_quantization.synthetic import random_compressed_store
+    cfg = Qwen3Config.from_dict(dict(QWEN3_14B, num_hidden_layers=layers))
+    store = random_compressed_store(cfg, seed=0, device=device)
+    backend = CompressedLinearBackend('marlin')
+    runtime = CompressedResidentRuntime(store, backend, device=device, verbose=False)
+    model = QuantizedQwen3ForCausalLM(store, runtime, device=device, linear_backend=backend)
+    torch.cuda.synchronize()
+    return cfg, model, runtime
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=20)
-    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--steps', type=int, default=127, help='timed decode tokens')
+    ap.add_argument('--warmup', type=int, default=5, help='untimed decode tokens before the timed ones')
     ap.add_argument('--layers', type=int, default=40)
     ap.add_argument('--cpu-budget', type=float, default=15.0, help='seconds for the CPU baseline sample')
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--no-extras', action='store_true', help='skip prefill / copy / per-kernel sections')
+    ap.add_argument('--no-extras', action='store_true', help='skip the GEMV pass, kernel and prefill sections')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path (every box has one GPU); '
               'run with --gpus 1', file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print('need --steps >= 1 and --warmup >= 0', file=sys.stderr)
         return 2
 
     import torch
@@ -173,111 +190,164 @@ def main() -> int:
         print('bench.py needs a GPU', file=sys.stderr)
         return 2
     device = torch.device('cuda:0')
-    native.load()
-    log(f'device {torch.cuda.get_device_name(0)}; building {args.layers} layers of weights')
-    layers = make_layer_weights(torch, native, args.layers, device)
+    torch.manual_seed(0)
 
-    xs = {HIDDEN: torch.randn(1, HIDDEN, device=device).half(), INTER: torch.randn(1, INTER, device=device).half()}
-    outs = {name: torch.empty(1, n, device=device, dtype=torch.float16) for name, _, n in LAYER_SHAPES}
+    log(f'building a random {args.layers}-layer Qwen3-14B-shaped W4A16 model and repacking it')
+    t0 = time.perf_counter()
+    cfg, model, runtime = build_model(torch, args.layers, device)
+    build_s = time.perf_counter() - t0
+    capacity = PROMPT + 1 + args.warmup + args.steps
+    prompt = torch.randint(0, cfg.vocab_size, (1, PROMPT), generator=torch.Generator().manual_seed(0)).to(device)
 
-    def step():
-        for layer in layers:
-            for name, k, n in LAYER_SHAPES:
-                tiles, meta, _, _ = layer[name]
-                native.w4a16_linear(xs[k], tiles, meta, n, GROUP, out=outs[name])
+    def generate(n_untimed: int, n_timed: int):
+        cache = model.make_resident_cache(batch_size=1, max_seq_len=capacity)
+        torch.cuda.synchronize()
+        t_p = time.perf_counter()
+        out = model(prompt, cache=cache, logits_to_keep=1)
+        token = out.logits[:, -1].argmax(dim=-1, keepdim=True)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t_p
+        for _ in range(n_untimed):
+            token = model(token, cache=cache, logits_to_keep=1).logits[:, -1].argmax(dim=-1, keepdim=True)
+        torch.cuda.synchronize()
+        t_d = time.perf_counter()
+        for _ in range(n_timed):
+            token = model(token, cache=cache, logits_to_keep=1).logits[:, -1].argmax(dim=-1, keepdim=True)
+        torch.cuda.synchronize()
+        return prefill_s, time.perf_counter() - t_d, cache
 
-    step()   # eager warm call (loads code objects)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    log(f'timing {args.steps} steps')
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    ms_per_step = start.elapsed_time(end) / args.steps
-    step_bytes = args.layers * sum(w4_bytes(1, n, k) for _, k, n in LAYER_SHAPES)
-    value = step_bytes / (ms_per_step / 1000.0) / 1e9
-
+    log('warm-up generation (captures the decode-step graph)')
+    t0 = time.perf_counter()
+    cache = model.make_resident_cache(batch_size=1, max_seq_len=capacity)
+    capture_s = time.perf_counter() - t0
+    del cache
+    generate(2, 0)
+    log(f'timed generation: prefill {PROMPT}, {args.warmup} untimed + {args.steps} timed decode tokens')
+    prefill_s, decode_s, cache = generate(args.warmup, args.steps)
+    assert cache.lengths[0] == PROMPT + args.warmup + args.steps
+    toks = args.steps / decode_s
+    weight_bytes = runtime.resident_storage_bytes
+    kv_bytes_per_token = 2 * args.layers * cfg.num_key_value_heads * cfg.head_dim * 2 * (PROMPT + args.warmup)
+    lm_bytes = cfg.vocab_size * cfg.hidden_size * 2
     result = {
-        'metric': METRIC, 'value': round(value, 2), 'unit': 'GB/s', 'n_gpus': 1, 'steps': args.steps,
-        'warmup': args.warmup, 'ms_per_step': round(ms_per_step, 4), 'higher_is_better': True,
-        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'fp16', 'data': 'synthetic',
-        'config': {'workload': 'configs[1]: W4A16 G=128 decode GEMV, M=1, Qwen3-14B projection shapes '
-                               f'(q,k,v,o,gate,up,down) x {args.layers} layers per step, HIP-graph replay',
-                   'layers': args.layers, 'launches_per_step': 7 * args.layers,
-                   'weight_bytes_resident': step_bytes, 'group_size': GROUP},
-        'pct_hbm_peak': round(100.0 * value / HBM_PEAK_GBS, 2),
-        'decode_projection_passes_per_s': round(1000.0 / ms_per_step, 2),
-        'wall_s_timed': round(wall, 4),
+        'metric': METRIC, 'value': round(toks, 3), 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': round(decode_s * 1000 / args.steps, 4), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': round(toks / PUBLISHED_TOKS, 3) if args.layers == 40 else None,
+        'dtype': 'fp16', 'data': 'synthetic',
+        'config': {'workload': f'configs[4]: Qwen3-14B-shaped AWQ-INT4 G=128 decoder ({args.layers} layers), random '
+                               f'weights, B=1, {PROMPT}-token random prompt, greedy decode, fp16 KV resident; '
+                               'one step = one decode token (graph replay + argmax)',
+                   'layers': args.layers, 'prompt_tokens': PROMPT, 'group_size': GROUP,
+                   'kv_capacity': capacity},
+        'prefill_seconds': round(prefill_s, 4),
+        'prefill_tok_s': round(PROMPT / prefill_s, 1),
+        'bytes_per_token': {'decoder_weights': int(weight_bytes), 'lm_head_fp16': lm_bytes,
+                            'kv_cache_read_at_start': kv_bytes_per_token},
+        'effective_gbs': round((weight_bytes + lm_bytes + kv_bytes_per_token) * toks / 1e9, 1),
+        'setup_seconds': {'build_and_repack': round(build_s, 2), 'graph_capture': round(capture_s, 3)},
     }
+    result['pct_hbm_peak_effective'] = round(100.0 * result['effective_gbs'] / HBM_PEAK_GBS, 2)
+    del cache
 
     if not args.no_extras:
-        # Per-shape kernel timing: a graph of the `layers` launches of one shape.
-        by_shape = []
+        layers = [runtime.weights_for(i) for i in range(args.layers)]
+        outs, xs = {}, {k: torch.randn(1, k, device=device).half() for k in (HIDDEN, INTER)}
+
+        def linear(x, prepared, out):
+            native.w4a16_linear(x, prepared.tiles, prepared.meta, prepared.n, GROUP, out=out,
+                                workspace=prepared.workspace)
+
+        # the 280 per-projection GEMVs of one decode token, as one graph.
         for name, k, n in LAYER_SHAPES:
-            if name in ('v_proj', 'up_proj'):
-                continue   # same shapes as k_proj / gate_proj
+            outs[name] = torch.empty(1, n, device=device, dtype=torch.float16)
+
+        def gemv_pass():
+            for w in layers:
+                for name, k, n in LAYER_SHAPES:
+                    linear(xs[k], w[name + '._prepared'], outs[name])
+
+        gemv_pass()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            gemv_pass()
+        sec = time_graph(torch, g, 10)
+        del g
+        pass_bytes = args.layers * sum(w4_bytes(1, n, k) for _, k, n in LAYER_SHAPES)
+        result['gemv_pass'] = {'workload': 'configs[1]: W4A16 G=128 decode GEMV, M=1, q,k,v,o,gate,up,down x '
+                                           f'{args.layers} layers per pass, HIP-graph replay',
+                               'gbs': round(pass_bytes / sec / 1e9, 1),
+                               'pct_hbm_peak': round(100.0 * pass_bytes / sec / 1e9 / HBM_PEAK_GBS, 2),
+                               'us_per_pass': round(sec * 1e6, 1), 'bytes_per_pass': pass_bytes}
+
+        # Kernels of the decode step, each as a graph of its `layers` launches.
+        kernels = []
+        step_ops = {s[0] for s in STEP_LINEARS}
+        extra = [s for s in LAYER_SHAPES if s[0] in ('self_attn.q_proj', 'self_attn.k_proj', 'mlp.gate_proj')]
+        for name, k, n in STEP_LINEARS + extra:
+            y = torch.empty(1, n, device=device, dtype=torch.float16)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                for layer in layers:
-                    tiles, meta, _, _ = layer[name]
-                    native.w4a16_linear(xs[k], tiles, meta, n, GROUP, out=outs[name])
-            per_launch = time_graph(torch, g, 10) / len(layers)
+                for w in layers:
+                    linear(xs[k], w[name + '._prepared'], y)
+            per = time_graph(torch, g, 10) / len(layers)
             b = w4_bytes(1, n, k)
-            by_shape.append({'shape': f'{k}->{n}', 'kernel': kernel_name_for((1, n, k)), 'bytes': b,
-                             'us_per_launch': round(per_launch * 1e6, 3),
-                             'gbs': round(b / per_launch / 1e9, 1),
-                             'frac': round(b / per_launch / 1e9 / HBM_PEAK_GBS, 4),
-                             'launches_per_step': args.layers * (2 if name in ('k_proj', 'gate_proj') else 1)})
-            del g
-        # dominant kernel = largest total time per step
-        for e in by_shape:
-            e['us_per_step'] = e['us_per_launch'] * e['launches_per_step']
-        kernels = {}
-        for e in by_shape:
-            agg = kernels.setdefault(e['kernel'], {'bytes': 0, 'us': 0.0, 'launches': 0})
-            agg['bytes'] += e['bytes'] * e['launches_per_step']
-            agg['us'] += e['us_per_step']
-            agg['launches'] += e['launches_per_step']
-        dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]['us'])
-        achieved = dom['bytes'] / (dom['us'] / 1e6) / 1e9
-        dom_shapes = [e['shape'] for e in by_shape if e['kernel'] == dom_name]
-        traffic = profiled_traffic(dom_name, dom_shapes[0]) if len(dom_shapes) == 1 else None
-        result['roofline'] = {
-            'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-            'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'kernel': dom_name,
-            'shapes': dom_shapes,
-            'avg_launch_us': round(dom['us'] / dom['launches'], 3),
-            'algorithmic_bytes_per_launch': dom['bytes'] // dom['launches'],
-        }
-        result['roofline_by_shape'] = by_shape
+            kernels.append({'op': name, 'shape': f'{k}->{n}', 'kernel': kernel_name_for((1, n, k)), 'bytes': b,
+                            'us_per_launch': round(per * 1e6, 3), 'gbs': round(b / per / 1e9, 1),
+                            'frac': round(b / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': name in step_ops,
+                            'launches_per_token': args.layers})
+            del g, y
+        # the attention kernel at the decode position of the timed steps
+        kc = [torch.randn(cfg.num_key_value_heads, capacity, 128, device=device).half() for _ in range(2)]
+        qkv = torch.randn(QKV, device=device).half()
+        cos, sin = model.rotary_emb.table(capacity, device)
+        pos = torch.tensor([PROMPT + args.warmup], dtype=torch.int32, device=device)
+        att_out = torch.empty(HIDDEN, device=device, dtype=torch.float16)
+        ws = torch.zeros(native.decode_attention_workspace_size(40, 8, 128, capacity), dtype=torch.uint8,
+                         device=device)
+        qn = torch.ones(128, device=device).half()
 
-        # Prefill GEMM (config 3), M=4096 on the first layer's weights.
+        def attn():
+            native.decode_attention(qkv, 40, 8, qn, qn, 1e-6, cos, sin, pos, kc[0], kc[1], 128 ** -0.5,
+                                    out=att_out, workspace=ws)
+        attn()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(args.layers):
+                attn()
+        per = time_graph(torch, g, 10) / args.layers
+        att_bytes = 2 * 8 * (PROMPT + args.warmup) * 128 * 2 + QKV * 2 + HIDDEN * 2
+        kernels.append({'op': 'attention', 'shape': f'GQA 40/8 x 128, {PROMPT + args.warmup + 1} keys',
+                        'kernel': 'decode_attention_kernel', 'bytes': att_bytes,
+                        'us_per_launch': round(per * 1e6, 3), 'gbs': round(att_bytes / per / 1e9, 1),
+                        'frac': round(att_bytes / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': True,
+                        'launches_per_token': args.layers})
+        del g, kc
+        for e in kernels:
+            e['us_per_token'] = round(e['us_per_launch'] * e['launches_per_token'], 2)
+        step = [e for e in kernels if e['in_decode_step']]
+        dom = max(step, key=lambda e: e['us_per_token'])
+        result['roofline'] = {
+            'bound': 'hbm', 'achieved': dom['gbs'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': dom['frac'],
+            'traffic': profiled_traffic(dom['kernel'], dom['shape']), 'kernel': dom['kernel'], 'shape': dom['shape'],
+            'op': dom['op'], 'avg_launch_us': dom['us_per_launch'], 'algorithmic_bytes_per_launch': dom['bytes'],
+        }
+        result['decode_step_kernels'] = kernels
+
+        # prefill GEMM, M=4096 on the first layer's weights.
         xp = {kk: torch.randn(4096, kk, device=device).half() for kk in (HIDDEN, INTER)}
         prefill = []
-        for name, k, n in LAYER_SHAPES:
-            if name in ('v_proj', 'up_proj'):
-                continue
-            tiles, meta, _, _ = layers[0][name]
+        for name, k, n in [('self_attn.q_proj', HIDDEN, HIDDEN), ('self_attn.k_proj', HIDDEN, KV),
+                           ('mlp.gate_proj', HIDDEN, INTER), ('mlp.down_proj', INTER, HIDDEN),
+                           ('self_attn.qkv_proj', HIDDEN, QKV), ('mlp.gate_up_proj', HIDDEN, GATE_UP)]:
             yp = torch.empty(4096, n, device=device, dtype=torch.float16)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                native.w4a16_linear(xp[k], tiles, meta, n, GROUP, out=yp)
+                linear(xp[k], layers[0][name + '._prepared'], yp)
             sec = time_graph(torch, g, 10)
             tflops = 2 * 4096 * n * k / sec / 1e12
-            prefill.append({'shape': f'{k}->{n}', 'M': 4096, 'us': round(sec * 1e6, 1), 'tflops': round(tflops, 1),
-                            'frac_fp16_mfma': round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)})
+            prefill.append({'op': name, 'shape': f'{k}->{n}', 'M': 4096, 'us': round(sec * 1e6, 1),
+                            'tflops': round(tflops, 1), 'frac_fp16_mfma': round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)})
             del g, yp
         result['prefill'] = prefill
 
@@ -299,7 +369,7 @@ def main() -> int:
 
     if not args.no_cpu_baseline:
         log('cpu baseline')
-        result['cpu_baseline'] = cpu_baseline(args.cpu_budget)
+        result['cpu_baseline'] = cpu_baseline(args.cpu_budget, args.layers)
 
     print(json.dumps(result), flush=True)
     return 0

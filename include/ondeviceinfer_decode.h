@@ -35,8 +35,10 @@ int wq_add_rmsnorm(const uint16_t* x, const uint16_t* delta, const uint16_t* wei
  * Replaces: `F.silu(gate) * up` (quantized_model.py:222-224). */
 int wq_silu_mul(const uint16_t* gate_up, int64_t rows, int64_t n, uint16_t* out, void* stream);
 
-/* Workspace bytes for wq_decode_attention at this geometry (zero-filled once
- * by the caller; every call leaves it zeroed). */
+/* Workspace bytes for wq_decode_attention at this geometry (0 when one
+ * workgroup covers each kv head's cache).  The workspace holds the chunk
+ * partials between the attention launch and its merge launch; it needs no
+ * initialization, and calls that may overlap need separate workspaces. */
 int wq_decode_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_seq,
                                        size_t* bytes);
 
@@ -50,8 +52,9 @@ int wq_decode_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_
  * Replaces: q/k rms_norm + apply_rotary_pos_emb + ResidentKVCache.update +
  * F.scaled_dot_product_attention(enable_gqa=True) for query_length 1
  * (quantized_model.py:171-199, layers.py:64-80, cache.py:60-80,
- * attention.py:35-85).  A position outside [0, max_seq) writes NaN to out and
- * leaves the cache untouched. */
+ * attention.py:35-85).  max_seq <= 8192, q_heads / kv_heads <= 8.  A
+ * position outside [0, max_seq) writes NaN to out and leaves the cache
+ * untouched. */
 int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                         const uint16_t* q_norm_weight, const uint16_t* k_norm_weight, float eps,
                         const uint16_t* cos_table, const uint16_t* sin_table, const int32_t* position,

@@ -103,6 +103,26 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
                     int64_t n, int64_t group_size, uint16_t* y,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* One decode-token (M = 1) W4A16 linear with the neighbouring elementwise
+ * work of the Qwen3 decoder layer folded in (n % 16 == 0):
+ *   x_mode 0  x as given ([k]);
+ *   x_mode 1  x <- norm_weight * fp16(x * rsqrt(sum(sumsq_in[0..sumsq_count)) / k + eps)),
+ *             the RMSNorm of x whose sum of squares the producing linear
+ *             left in sumsq_in (one float per 16-row tile, at most 512);
+ *   x_mode 2  x is [gate | up] of length 2k and x <- fp16(fp16(silu(gate)) * up);
+ *   residual  if not NULL, y = residual + fp16(x . W^T) (fp16 add; may alias y);
+ *   sumsq_out if not NULL, receives the sum of squares of y per 16-row tile
+ *             (n / 16 floats) for the next linear's x_mode 1.
+ * Workspace as for wq_w4a16_linear at m = 1.  Replaces, per decode token,
+ * rms_norm before q/k/v and gate/up, `residual + attention_output`,
+ * `residual + mlp_output` and `F.silu(gate) * up` around the linears
+ * (quantized_model.py:146-227); no counterpart kernel exists in the
+ * reference (it runs them as separate torch ops). */
+int wq_w4a16_decode_fused(const uint16_t* x, int64_t k, const void* tiles, const void* meta, int64_t n,
+                          int64_t group_size, int32_t x_mode, const uint16_t* norm_weight, const float* sumsq_in,
+                          int64_t sumsq_count, float eps, const uint16_t* residual, float* sumsq_out, uint16_t* y,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------- W8 (int8, per-output-channel scale) */
 
 /* fp16 [n, k] = fp16(q * scale[n]), scale fp32 [n].  Replaces the INT8 branch

@@ -30,6 +30,7 @@ WQ_ERR_WORKSPACE = 4
 ABI_VERSION = 1
 
 W4_BLOCK_K = 128
+DECODE_ATTENTION_MAX_SEQ = 8192   # wq_decode_attention: 64 workgroups x 2 sub-chunks x 64 positions per kv head
 W4_META_BYTES = 40
 W8_BLOCK_K = 128
 
@@ -47,6 +48,8 @@ _SIGNATURES = {
     'wq_w4_decode': [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P],
     'wq_w4a16_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
     'wq_w4a16_linear': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, ctypes.c_size_t, _P],
+    'wq_w4a16_decode_fused': [_P, _I64, _P, _P, _I64, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P,
+                              _P, _P, ctypes.c_size_t, _P],
     'wq_w8_decode': [_P, _P, _I64, _I64, _P, _P],
     'wq_w8a16_workspace_size': [_I64, _I64, _I64, _SIZE_P],
     'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
@@ -276,6 +279,44 @@ def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: in
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     _call('wq_w4a16_linear', _ptr(x), m, k, _ptr(tiles), _ptr(meta), n, group_size, _ptr(out), ws_ptr, ws_bytes,
           _stream(device))
+    return out
+
+
+X_PLAIN, X_RMSNORM, X_SILU_MUL = 0, 1, 2
+
+
+def w4a16_decode_fused(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: int, group_size: int, *,
+                       x_mode: int = X_PLAIN, norm_weight: torch.Tensor | None = None,
+                       sumsq_in: torch.Tensor | None = None, eps: float = 1e-6,
+                       residual: torch.Tensor | None = None, sumsq_out: torch.Tensor | None = None,
+                       out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode-token W4A16 linear with the fused prologue/epilogue of
+    ``wq_w4a16_decode_fused`` (x_mode ``X_PLAIN`` / ``X_RMSNORM`` /
+    ``X_SILU_MUL``; ``residual`` added in fp16; per-tile ``sumsq_out``)."""
+    device = _require_gpu(x, tiles, meta, norm_weight, sumsq_in, residual, sumsq_out, out, workspace)
+    if x.dtype != torch.float16 or not x.is_contiguous():
+        raise TypeError('x must be a contiguous float16 tensor')
+    k = x.numel() // 2 if x_mode == X_SILU_MUL else x.numel()
+    if norm_weight is not None:
+        _check(norm_weight, torch.float16, (k,), 'norm_weight')
+    if sumsq_in is not None and (sumsq_in.dtype != torch.float32 or not sumsq_in.is_contiguous()):
+        raise TypeError('sumsq_in must be contiguous float32')
+    if sumsq_out is not None:
+        _check(sumsq_out, torch.float32, ((n + 15) // 16,), 'sumsq_out')
+    if residual is not None:
+        if residual.dtype != torch.float16 or residual.numel() != n or not residual.is_contiguous():
+            raise ValueError(f'residual must be contiguous float16 with {n} elements')
+    if out is None:
+        out = torch.empty((1, n), dtype=torch.float16, device=device)
+    elif out.dtype != torch.float16 or out.numel() != n or not out.is_contiguous():
+        raise ValueError(f'out must be contiguous float16 with {n} elements')
+    if workspace is None:
+        workspace = shared_workspace(device, w4a16_workspace_size(1, n, k, group_size))
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                             workspace.numel() * workspace.element_size())
+    _call('wq_w4a16_decode_fused', _ptr(x), k, _ptr(tiles), _ptr(meta), n, group_size, x_mode, _ptr(norm_weight),
+          _ptr(sumsq_in), 0 if sumsq_in is None else sumsq_in.numel(), float(eps), _ptr(residual), _ptr(sumsq_out),
+          _ptr(out), ws_ptr, ws_bytes, _stream(device))
     return out
 
 

@@ -27,6 +27,11 @@ int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const ui
 int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
                    half_t* y, hipStream_t s);
 
+int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
+                         int x_mode, const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
+                         const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
+                         hipStream_t s);
+
 // Largest M served by the MFMA GEMV (4 chunks of 16 activation rows).
 constexpr int64_t kSkinnyMaxM = 64;
 
@@ -86,6 +91,29 @@ extern "C" int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const vo
                             workspace_bytes, as_stream(stream));
   return launch_w4_gemm(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
                         reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
+}
+
+extern "C" int wq_w4a16_decode_fused(const uint16_t* x, int64_t k, const void* tiles, const void* meta, int64_t n,
+                                     int64_t group_size, int32_t x_mode, const uint16_t* norm_weight,
+                                     const float* sumsq_in, int64_t sumsq_count, float eps, const uint16_t* residual,
+                                     float* sumsq_out, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  if (int st = linear_shape_check(1, n, k)) return st;
+  WQ_REQUIRE(n % 16 == 0 && group_size % kW4BlockK == 0 && group_size > 0 && k % group_size == 0,
+             WQ_ERR_UNSUPPORTED, "fused decode linear needs n %% 16 == 0, group_size %% 128 == 0, k %% group_size == 0 "
+             "(n=%lld k=%lld group=%lld)", (long long)n, (long long)k, (long long)group_size);
+  WQ_REQUIRE(x_mode >= 0 && x_mode <= 2, WQ_ERR_INVALID_ARGUMENT, "x_mode must be 0 (plain), 1 (rmsnorm) or 2 (silu_mul)");
+  WQ_REQUIRE(x && tiles && meta && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(x_mode != 1 || (norm_weight && sumsq_in && sumsq_count > 0 && sumsq_count <= 512),
+             WQ_ERR_INVALID_ARGUMENT, "rmsnorm mode needs norm_weight, sumsq_in and 0 < sumsq_count <= 512");
+  WQ_REQUIRE(aligned16(x) && aligned16(tiles) && aligned16(y) && (reinterpret_cast<uintptr_t>(meta) & 7u) == 0 &&
+                 aligned16(norm_weight) && (reinterpret_cast<uintptr_t>(residual) & 7u) == 0,
+             WQ_ERR_INVALID_ARGUMENT, "x, tiles, y and norm_weight must be 16-byte aligned, meta and residual 8-byte");
+  return launch_w4_gemv_fused(reinterpret_cast<const half_t*>(x), (int)k, reinterpret_cast<const uint4_t*>(tiles),
+                              reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, x_mode,
+                              reinterpret_cast<const half_t*>(norm_weight), sumsq_in, (int)sumsq_count, eps,
+                              reinterpret_cast<const half_t*>(residual), sumsq_out, reinterpret_cast<half_t*>(y),
+                              workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight, const uint16_t* scale,

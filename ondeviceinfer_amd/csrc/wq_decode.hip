@@ -18,9 +18,11 @@ namespace wq {
 namespace {
 
 constexpr int kHeadDim = 128;     // Qwen3 head_dim; one lane holds two elements
-constexpr int kChunk = 64;        // KV positions per attention workgroup
+constexpr int kSub = 64;          // KV positions per attention sub-chunk (one per lane of a softmax wave)
 constexpr int kMaxGroup = 8;      // q heads per kv head
-constexpr int kMaxChunks = 256;   // so the combine's staging fits the reduction buffer
+constexpr int kMaxChunks = 64;    // attention workgroups per kv head
+constexpr int kMaxSpc = 2;        // sub-chunks per workgroup
+constexpr int kMaxSeq = kMaxChunks * kMaxSpc * kSub;
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -32,6 +34,27 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
   return v;
+}
+
+// Reductions over the 16 lanes of a DPP row (every lane gets the result):
+// quad swaps, then the half-row and row mirrors.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_f<0xb1>(v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4e>(v));    // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+  return fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_f<0xb1>(v);
+  v += dpp_f<0x4e>(v);
+  v += dpp_f<0x141>(v);
+  return v + dpp_f<0x140>(v);
 }
 
 // ------------------------------------------------------------------ RMSNorm
@@ -117,213 +140,274 @@ __device__ __forceinline__ half2_t norm_rope_pair(half2_t v, const half_t* nw, f
   return t1 + t2;
 }
 
-// grid = (kv_heads, chunks of 64 positions over max_seq); 256 threads.
-// Chunk c of kv head h scores its positions against the head's G query
-// heads, keeps its softmax partial (max, sum, unnormalized output) and the
-// last chunk to finish merges all partials in chunk order.  The workgroup
-// whose chunk holds `pos` also normalizes, rotates and appends the new key
-// and value, and uses them from LDS.
-__global__ __launch_bounds__(256) void decode_attention_kernel(
+// Split of a kv head's positions over workgroups: `spc` (1 or 2) sub-chunks
+// of 64 positions per workgroup, so that no head has more than kMaxChunks
+// workgroups (the merge reads one partial per workgroup).
+struct AttnSplit {
+  int spc, nc;
+};
+
+AttnSplit attn_split(int64_t max_seq) {
+  const int64_t subs = (max_seq + kSub - 1) / kSub;
+  const int spc = (int)((subs + kMaxChunks - 1) / kMaxChunks);
+  return {spc, (int)((subs + spc - 1) / spc)};
+}
+
+// grid = (kv_heads, chunks); 256 threads = 4 waves.  Workgroup c of kv head
+// h covers positions [c * SPC * 64, (c + 1) * SPC * 64) in sub-chunks of 64,
+// with an online softmax over the head's G <= 8 query heads:
+//   loads   every K fragment and V row this workgroup needs is requested
+//           before the q/k prologue (rows clamped into the cache; rows past
+//           L or at `pos` are replaced below);
+//   scores  S[g][p] = q_g . k_p on the matrix cores: A = the query heads
+//           (rows g, zero past G), B = 16 key rows per wave (each lane 16
+//           bytes of one row), four k-steps of 32 elements;
+//   softmax DPP row r (16 lanes x 4 positions) of wave w owns query head
+//           4w + r: running max / sum and the rescale factor;
+//   P.V     lane (dg, q) of wave w: elements 8dg .. 8dg+7 of positions
+//           4(q + 4w) .. +3, one 16-byte V load per position, one float4
+//           of P per head; the four position quads of a wave are summed
+//           with shuffles at the end.
+// The workgroup whose chunk holds `pos` also normalizes, rotates and
+// appends the new key and value, and takes them from LDS.  With one chunk
+// per head the workgroup writes the output; otherwise each chunk writes its
+// (max, sum, unnormalized output) to the workspace and
+// decode_attention_merge_kernel, launched next, combines them.
+template <int G, int SPC>
+__global__ __launch_bounds__(256, 2) void decode_attention_kernel(
     const half_t* __restrict__ qkv, int H, int KV, const half_t* __restrict__ qn_w,
     const half_t* __restrict__ kn_w, float eps, const half_t* __restrict__ cos_t, const half_t* __restrict__ sin_t,
     const int32_t* __restrict__ position, half_t* kc, half_t* vc, int max_seq, float scale,
-    half_t* __restrict__ out, float* ws_o, float* ws_ml, uint32_t* ws_cnt) {
-  constexpr int D = kHeadDim, C = kChunk, GM = kMaxGroup;
-  __shared__ float qs[GM][D];
+    half_t* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  constexpr int D = kHeadDim, C = kSub, GM = kMaxGroup;
+  __shared__ __attribute__((aligned(16))) half_t qh[GM][D];
   __shared__ __attribute__((aligned(16))) half_t knew[D];
   __shared__ __attribute__((aligned(16))) half_t vnew[D];
-  __shared__ float sc[GM][C];
-  __shared__ float red[4 * GM * D];   // P.V partials per position group; later the combine's staging
+  __shared__ __attribute__((aligned(16))) float sc[GM][C];
+  __shared__ float alph[GM];
+  __shared__ __attribute__((aligned(16))) float red[4 * GM * D];   // per-wave P.V partials; later the merge's staging
   __shared__ float mls[GM][2];
-  __shared__ uint32_t s_prev;
 
   const int h = blockIdx.x, chunk = blockIdx.y, NC = gridDim.y;
-  const int G = H / KV;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = lane & 15, kb = lane >> 4;
   const int pos = *position;
   if (pos < 0 || pos >= max_seq) {
     if (h == 0 && chunk == 0)
-      for (int i = tid; i < H * D; i += 256) out[i] = (half_t)__builtin_nanf("");
+      for (int j = tid; j < H * D; j += 256) out[j] = (half_t)__builtin_nanf("");
     return;
   }
   const int L = pos + 1;
-  const int p0 = chunk * C;
+  const int p0 = chunk * SPC * C;
   const bool active = p0 < L;
-  const bool owner = pos >= p0 && pos < p0 + C;
-  const size_t head_base = (size_t)h * max_seq * D;
+  const bool owner = pos >= p0 && pos < p0 + SPC * C;
+  const half_t* kh = kc + (size_t)h * max_seq * D;
+  const half_t* vh = vc + (size_t)h * max_seq * D;
+  const int dg = lane & 15, pq = (lane >> 4) + 4 * wave;   // P.V: elements 8dg.., positions 4pq..4pq+3
 
-  // Issue this chunk's K and V loads first (row pos is produced below).
-  const int pl = tid >> 2, part = tid & 3;   // scores: position p0 + pl, elements [32 part, 32 part + 32)
-  const int pk = p0 + pl;
-  uint4_t kr[4] = {};
-  if (active && pk < L && pk != pos) {
-    const uint4_t* src = reinterpret_cast<const uint4_t*>(kc + head_base + (size_t)pk * D + part * 32);
+  uint4_t kr[SPC][4], vr[SPC][4];
+  if (active) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kr[j] = src[j];
-  }
-  const int dp = tid & 63, pg = tid >> 6;    // P.V: elements 2dp, 2dp+1 of positions p0 + 16 pg + j
-  uint32_t vr[16];
+    for (int s = 0; s < SPC; ++s) {
+      const int rk = min(p0 + s * C + 16 * wave + i, max_seq - 1);
+      const uint4_t* ks_src = reinterpret_cast<const uint4_t*>(kh + (size_t)rk * D + 8 * kb);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int p = p0 + 16 * pg + j;
-    vr[j] = (active && p < L && p != pos)
-                ? reinterpret_cast<const uint32_t*>(vc + head_base + (size_t)p * D)[dp]
-                : 0u;
+      for (int ks = 0; ks < 4; ++ks) kr[s][ks] = ks_src[4 * ks];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rv = min(p0 + s * C + 4 * pq + e, max_seq - 1);
+        vr[s][e] = *reinterpret_cast<const uint4_t*>(vh + (size_t)rv * D + 8 * dg);
+      }
+    }
   }
 
   if (active) {
     const half_t* cs = cos_t + (size_t)pos * D;
     const half_t* sn = sin_t + (size_t)pos * D;
-    for (int g = wave; g < G; g += 4) {
-      const half2_t v = reinterpret_cast<const half2_t*>(qkv + (size_t)(h * G + g) * D)[lane];
-      const half2_t r = norm_rope_pair(v, qn_w, eps, cs, sn, lane);
-      qs[g][2 * lane] = (float)r[0];
-      qs[g][2 * lane + 1] = (float)r[1];
+    for (int g = wave; g < GM; g += 4) {
+      half2_t r = {};
+      if (g < G) {
+        const half2_t v = reinterpret_cast<const half2_t*>(qkv + (size_t)(h * G + g) * D)[lane];
+        r = norm_rope_pair(v, qn_w, eps, cs, sn, lane);
+      }
+      reinterpret_cast<half2_t*>(qh[g])[lane] = r;
     }
     if (owner && wave == 0) {
       const half2_t v = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + h) * D)[lane];
       const half2_t r = norm_rope_pair(v, kn_w, eps, cs, sn, lane);
       reinterpret_cast<half2_t*>(knew)[lane] = r;
-      reinterpret_cast<half2_t*>(kc + head_base + (size_t)pos * D)[lane] = r;
+      reinterpret_cast<half2_t*>(kc + (size_t)h * max_seq * D + (size_t)pos * D)[lane] = r;
     }
     if (owner && wave == 1) {
       const half2_t v = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + KV + h) * D)[lane];
       reinterpret_cast<half2_t*>(vnew)[lane] = v;
-      reinterpret_cast<half2_t*>(vc + head_base + (size_t)pos * D)[lane] = v;
+      reinterpret_cast<half2_t*>(vc + (size_t)h * max_seq * D + (size_t)pos * D)[lane] = v;
     }
   }
   __syncthreads();
 
+  float o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[g][k] = 0.f;
+  const int srow = lane >> 4, sj = lane & 15, sg = 4 * wave + srow;
+  float m_run = -INFINITY, l_run = 0.f;
+
   if (active) {
-    float s[GM];
+    half8_t qa[4];
 #pragma unroll
-    for (int g = 0; g < GM; ++g) s[g] = 0.f;
-    if (pk < L) {
-      half8_t kv[4];
+    for (int ks = 0; ks < 4; ++ks)
+      qa[ks] = i < GM ? *reinterpret_cast<const half8_t*>(&qh[i < GM ? i : 0][32 * ks + 8 * kb]) : half8_t{};
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        kv[j] = pk == pos ? reinterpret_cast<const half8_t*>(knew + part * 32)[j] : __builtin_bit_cast(half8_t, kr[j]);
+    for (int s = 0; s < SPC; ++s) {
+      const int ps = p0 + s * C;
+      if (ps < L) {
+        const int pk = ps + 16 * wave + i;
+        if (pk == pos) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kf = (float)kv[j][e];
-#pragma unroll
-          for (int g = 0; g < GM; ++g)
-            if (g < G) s[g] += qs[g][part * 32 + 8 * j + e] * kf;
+          for (int ks = 0; ks < 4; ++ks) kr[s][ks] = *reinterpret_cast<const uint4_t*>(knew + 32 * ks + 8 * kb);
         }
-    }
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int g = 0; g < GM; ++g) {
-      s[g] += __shfl_xor(s[g], 1);
-      s[g] += __shfl_xor(s[g], 2);
-    }
-    if (part == 0)
-      for (int g = 0; g < G; ++g) sc[g][pl] = pk < L ? s[g] * scale : -INFINITY;
-  }
-  __syncthreads();
-
-  if (active) {
-    // An active chunk holds position p0 < L, so every row max is finite.
-    for (int g = wave; g < G; g += 4) {
-      const float v = sc[g][lane];
-      const float m = wave_max(v);
-      const float e = v == -INFINITY ? 0.f : expf(v - m);
-      const float l = wave_sum(e);
-      sc[g][lane] = e;
-      if (lane == 0) {
-        mls[g][0] = m;
-        mls[g][1] = l;
-      }
-    }
-  }
-  __syncthreads();
-
-  if (active) {
-    float a0[GM], a1[GM];
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16(qa[ks], __builtin_bit_cast(half8_t, kr[s][ks]), acc);
+        if (kb < 2) {
 #pragma unroll
-    for (int g = 0; g < GM; ++g) a0[g] = a1[g] = 0.f;
+          for (int v = 0; v < 4; ++v) sc[4 * kb + v][16 * wave + i] = pk < L ? acc[v] * scale : -INFINITY;
+        }
+        __syncthreads();
+        if (sg < G) {
+          float4_t x = *reinterpret_cast<const float4_t*>(&sc[sg][4 * sj]);
+          const float m_new = fmaxf(m_run, row_max16(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))));   // finite
+          float es = 0.f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int q = 16 * pg + j;
-      if (p0 + q < L) {
-        const half2_t v2 = p0 + q == pos ? reinterpret_cast<const half2_t*>(vnew)[dp] : as_h2(vr[j]);
-        const float v0 = (float)v2[0], v1 = (float)v2[1];
-#pragma unroll
-        for (int g = 0; g < GM; ++g)
-          if (g < G) {
-            const float pr = sc[g][q];
-            a0[g] += pr * v0;
-            a1[g] += pr * v1;
+          for (int e = 0; e < 4; ++e) {
+            x[e] = x[e] == -INFINITY ? 0.f : expf(x[e] - m_new);
+            es += x[e];
           }
+          const float a = expf(m_run - m_new);   // 0 on the first sub-chunk
+          l_run = l_run * a + row_sum16(es);
+          m_run = m_new;
+          *reinterpret_cast<float4_t*>(&sc[sg][4 * sj]) = x;
+          if (sj == 0) alph[sg] = a;
+        }
+        __syncthreads();
+        // Rows past L carry P = 0; row `pos` comes from LDS, clamped or stale
+        // rows are zeroed so that 0 * garbage cannot produce NaN.
+        half8_t v8[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int p = ps + 4 * pq + e;
+          v8[e] = p == pos ? *reinterpret_cast<const half8_t*>(vnew + 8 * dg)
+                           : (p < L ? __builtin_bit_cast(half8_t, vr[s][e]) : half8_t{});
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float a = alph[g];
+          const float4_t pr = *reinterpret_cast<const float4_t*>(&sc[g][4 * pq]);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            float t = o[g][k] * a;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t += pr[e] * (float)v8[e][k];
+            o[g][k] = t;
+          }
+        }
+        __syncthreads();
       }
     }
-    for (int g = 0; g < G; ++g) {
-      red[(pg * GM + g) * D + 2 * dp] = a0[g];
-      red[(pg * GM + g) * D + 2 * dp + 1] = a1[g];
+    if (sg < G && sj == 0) {
+      mls[sg][0] = m_run;
+      mls[sg][1] = l_run;
+    }
+    // Sum the four position quads of this wave (lanes dg, dg+16, dg+32, dg+48).
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float t = o[g][k];
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        o[g][k] = t;
+      }
+    if (lane < 16) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float* dst = red + (wave * GM + g) * D + 8 * dg;
+        *reinterpret_cast<float4_t*>(dst) = float4_t{o[g][0], o[g][1], o[g][2], o[g][3]};
+        *reinterpret_cast<float4_t*>(dst + 4) = float4_t{o[g][4], o[g][5], o[g][6], o[g][7]};
+      }
     }
   }
   __syncthreads();
 
   if (NC == 1) {
-    for (int i = tid; i < G * D; i += 256) {
-      const int g = i / D, d = i % D;
+    for (int j = tid; j < G * D; j += 256) {
+      const int g = j / D, d = j % D;
       const float o = red[g * D + d] + red[(GM + g) * D + d] + red[(2 * GM + g) * D + d] + red[(3 * GM + g) * D + d];
       out[(size_t)(h * G + g) * D + d] = (half_t)(o / mls[g][1]);
     }
     return;
   }
-
-  // Publish this chunk's partial (device-coherent stores), then count it.
+  // Several chunks: publish this chunk's partial for decode_attention_merge
+  // (the next launch on the stream).
   if (active) {
-    float* po = ws_o + ((size_t)(h * NC + chunk) * G) * D;
-    for (int i = tid; i < G * D; i += 256) {
-      const int g = i / D, d = i % D;
-      const float o = red[g * D + d] + red[(GM + g) * D + d] + red[(2 * GM + g) * D + d] + red[(3 * GM + g) * D + d];
-      __hip_atomic_store(po + i, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < G * (D / 4)) {
+      const int g = tid / (D / 4), d = 4 * (tid % (D / 4));
+      float4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = red[g * D + d + e] + red[(GM + g) * D + d + e] + red[(2 * GM + g) * D + d + e] +
+               red[(3 * GM + g) * D + d + e];
+      *reinterpret_cast<float4_t*>(ws_o + (((size_t)(h * NC + chunk) * G + g) * D + d)) = o;
     }
-    if (tid < 2 * G)
-      __hip_atomic_store(ws_ml + ((size_t)(h * NC + chunk) * G) * 2 + tid, mls[tid >> 1][tid & 1], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < 2 * G) ws_ml[((size_t)(h * NC + chunk) * G) * 2 + tid] = mls[tid >> 1][tid & 1];
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) s_prev = __hip_atomic_fetch_add(&ws_cnt[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (s_prev != (uint32_t)(NC - 1)) return;
+}
 
-  // Last chunk to arrive: merge the active chunks' partials in chunk order.
-  const int NA = (L + C - 1) / C;
-  float* stm = red;                     // [NA][G] maxima
-  float* stl = red + kMaxChunks * GM;   // [NA][G] sums
-  for (int i = tid; i < NA * G; i += 256) {
-    const float* src = ws_ml + ((size_t)h * NC * G + i) * 2;
-    stm[i] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    stl[i] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Merge of the chunk partials of one query head: grid = q_heads, 128 threads
+// (one output element each).  All of the head's partial outputs are
+// requested before the maxima are known, then combined in chunk order:
+// out = sum_c exp(m_c - M) O_c / sum_c exp(m_c - M) l_c.
+__global__ __launch_bounds__(128) void decode_attention_merge_kernel(const int32_t* __restrict__ position, int G,
+                                                                     int NC, int chunk_positions, int max_seq,
+                                                                     const float* __restrict__ ws_o,
+                                                                     const float* __restrict__ ws_ml,
+                                                                     half_t* __restrict__ out) {
+  constexpr int D = kHeadDim;
+  __shared__ float ms[kMaxChunks], ls[kMaxChunks];
+  const int qh = blockIdx.x, h = qh / G, g = qh % G, d = threadIdx.x;
+  const int pos = *position;
+  if (pos < 0 || pos >= max_seq) return;   // the attention launch already wrote NaN
+  const int NA = min((pos + chunk_positions) / chunk_positions, NC);   // chunks holding positions 0..pos
+  float part[kMaxChunks];
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c)
+    part[c] = c < NA ? ws_o[((size_t)(h * NC + c) * G + g) * D + d] : 0.f;
+  if (d < NA) {
+    ms[d] = ws_ml[((size_t)(h * NC + d) * G + g) * 2];
+    ls[d] = ws_ml[((size_t)(h * NC + d) * G + g) * 2 + 1];
   }
   __syncthreads();
-  for (int i = tid; i < G * D; i += 256) {
-    const int g = i / D;
-    float M = -INFINITY;
-    for (int c = 0; c < NA; ++c) M = fmaxf(M, stm[c * G + g]);
-    float num = 0.f, den = 0.f;
-    for (int c = 0; c < NA; ++c) {
-      const float wgt = expf(stm[c * G + g] - M);
-      num += wgt * __hip_atomic_load(ws_o + ((size_t)(h * NC + c) * G) * D + i, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-      den += wgt * stl[c * G + g];
+  float M = -INFINITY;
+  for (int c = 0; c < NA; ++c) M = fmaxf(M, ms[c]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c)
+    if (c < NA) {
+      const float w = expf(ms[c] - M);
+      num += w * part[c];
+      den += w * ls[c];
     }
-    out[(size_t)h * G * D + i] = (half_t)(num / den);
-  }
-  if (tid == 0) __hip_atomic_store(&ws_cnt[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  out[(size_t)qh * D + d] = (half_t)(num / den);
 }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t attention_workspace_bytes(int64_t H, int64_t KV, int64_t max_seq) {
-  const int64_t nc = (max_seq + kChunk - 1) / kChunk;
+  const int64_t nc = attn_split(max_seq).nc;
   const int64_t g = H / KV;
-  return nc <= 1 ? 0 : align256((size_t)KV * 4) + align256((size_t)KV * nc * g * 2 * 4) + (size_t)KV * nc * g * kHeadDim * 4;
+  return nc <= 1 ? 0 : align256((size_t)KV * nc * g * 2 * 4) + (size_t)KV * nc * g * kHeadDim * 4;
 }
 
 int attention_shape_check(int64_t H, int64_t KV, int64_t head_dim, int64_t max_seq) {
@@ -333,8 +417,7 @@ int attention_shape_check(int64_t H, int64_t KV, int64_t head_dim, int64_t max_s
   WQ_REQUIRE(H % KV == 0, WQ_ERR_INVALID_ARGUMENT, "q_heads (%lld) must be a multiple of kv_heads (%lld)",
              (long long)H, (long long)KV);
   WQ_REQUIRE(H / KV <= kMaxGroup, WQ_ERR_UNSUPPORTED, "at most %d query heads per kv head", kMaxGroup);
-  WQ_REQUIRE(max_seq <= (int64_t)kMaxChunks * kChunk, WQ_ERR_UNSUPPORTED, "max_seq must be <= %d",
-             kMaxChunks * kChunk);
+  WQ_REQUIRE(max_seq <= kMaxSeq, WQ_ERR_UNSUPPORTED, "max_seq must be <= %d", kMaxSeq);
   WQ_REQUIRE(KV <= 65535, WQ_ERR_UNSUPPORTED, "too many kv heads");
   return WQ_OK;
 }
@@ -392,21 +475,40 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
              "null pointer argument");
   WQ_REQUIRE(((uintptr_t)qkv | (uintptr_t)key_cache | (uintptr_t)value_cache) % 16 == 0, WQ_ERR_INVALID_ARGUMENT,
              "qkv and the caches must be 16-byte aligned");
-  const int64_t nc = (max_seq + kChunk - 1) / kChunk;
+  const AttnSplit split = attn_split(max_seq);
+  const int64_t nc = split.nc;
   const size_t need = attention_workspace_bytes(q_heads, kv_heads, max_seq);
   WQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), WQ_ERR_WORKSPACE,
              "decode attention needs a zero-filled workspace of %zu bytes (got %zu)", need, workspace_bytes);
-  uint32_t* cnt = reinterpret_cast<uint32_t*>(workspace);
-  float* ml = need ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256((size_t)kv_heads * 4))
-                   : nullptr;
-  float* po = need ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ml) +
+  float* ml = need ? reinterpret_cast<float*>(workspace) : nullptr;
+  float* po = need ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) +
                                               align256((size_t)kv_heads * nc * (q_heads / kv_heads) * 2 * 4))
                    : nullptr;
-  hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)kv_heads, (unsigned)nc), dim3(256), 0, as_stream(stream),
-                     reinterpret_cast<const half_t*>(qkv), (int)q_heads, (int)kv_heads,
-                     reinterpret_cast<const half_t*>(q_norm_weight), reinterpret_cast<const half_t*>(k_norm_weight), eps,
-                     reinterpret_cast<const half_t*>(cos_table), reinterpret_cast<const half_t*>(sin_table), position,
-                     reinterpret_cast<half_t*>(key_cache), reinterpret_cast<half_t*>(value_cache), (int)max_seq, scale,
-                     reinterpret_cast<half_t*>(out), po, ml, cnt);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)kv_heads, (unsigned)nc), dim3(256), 0, as_stream(stream),
+                       reinterpret_cast<const half_t*>(qkv), (int)q_heads, (int)kv_heads,
+                       reinterpret_cast<const half_t*>(q_norm_weight), reinterpret_cast<const half_t*>(k_norm_weight),
+                       eps, reinterpret_cast<const half_t*>(cos_table), reinterpret_cast<const half_t*>(sin_table),
+                       position, reinterpret_cast<half_t*>(key_cache), reinterpret_cast<half_t*>(value_cache),
+                       (int)max_seq, scale, reinterpret_cast<half_t*>(out), po, ml);
+  };
+  const int g = (int)(q_heads / kv_heads);
+#define WQ_ATTN_CASE(GG)                                                                     \
+  case GG:                                                                                   \
+    if (split.spc == 1) launch(decode_attention_kernel<GG, 1>); else launch(decode_attention_kernel<GG, 2>); \
+    break;
+  switch (g) {
+    WQ_ATTN_CASE(1) WQ_ATTN_CASE(2) WQ_ATTN_CASE(3) WQ_ATTN_CASE(4)
+    WQ_ATTN_CASE(5) WQ_ATTN_CASE(6) WQ_ATTN_CASE(7) WQ_ATTN_CASE(8)
+    default: return fail(WQ_ERR_UNSUPPORTED, "query heads per kv head out of range");
+  }
+#undef WQ_ATTN_CASE
+  if (nc > 1) {
+    const int rc2 = check_launch("decode_attention");
+    if (rc2 != WQ_OK) return rc2;
+    hipLaunchKernelGGL(decode_attention_merge_kernel, dim3((unsigned)q_heads), dim3(kHeadDim), 0, as_stream(stream),
+                       position, g, (int)nc, split.spc * kSub, (int)max_seq, po, ml, reinterpret_cast<half_t*>(out));
+    return check_launch("decode_attention_merge");
+  }
   return check_launch("decode_attention");
 }

@@ -292,11 +292,57 @@ __device__ __forceinline__ int blk_kcol(int kb, int w) {
   return F == WFmt::W4 ? kb * 32 + 8 * w : kb * 16 + 8 * (w & 1) + 64 * (w >> 1);
 }
 
-template <int NB, int MM, WFmt F>
-__global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F>())) void gemv_flat_kernel(
+// Decode-step fusions of the flat GEMV (M = 1, W4): how x is formed while it
+// is staged, and the residual / sum-of-squares epilogue.
+enum class XMode {
+  Plain,     // x as given
+  RmsNorm,   // x <- w * fp16(x * rsqrt(sum(sumsq_in) / K + eps)): the next RMSNorm
+  SiluMul,   // x is [gate | up] of length 2K: x <- fp16(fp16(silu(gate)) * up)
+};
+
+struct FuseArgs {
+  const half_t* norm_w;    // RmsNorm: weight [K]
+  const float* sumsq_in;   // RmsNorm: sums of squares of x, one per 16-row tile of its producer (<= 512)
+  int sumsq_count;
+  float eps;
+  const half_t* residual;  // y = residual + x.W^T (fp16 add); may alias y
+  float* sumsq_out;        // per-16-row tile sum of squares of y (for the next RmsNorm)
+};
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Eight x values -> w * fp16(x * r), the reference's rms_norm order
+// (normalize in fp32, cast, scale in fp16).
+__device__ __forceinline__ uint4_t rms_scale8(uint4_t xv, uint4_t wv, float r) {
+  const half8_t xh = __builtin_bit_cast(half8_t, xv), wh = __builtin_bit_cast(half8_t, wv);
+  half8_t o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = wh[e] * (half_t)((float)xh[e] * r);
+  return __builtin_bit_cast(uint4_t, o);
+}
+
+// Eight (gate, up) pairs -> fp16(fp16(silu(gate)) * up), as F.silu on an
+// fp16 tensor followed by an fp16 product.
+__device__ __forceinline__ uint4_t silu_mul8(uint4_t gv, uint4_t uv) {
+  const half8_t gh = __builtin_bit_cast(half8_t, gv), uh = __builtin_bit_cast(half8_t, uv);
+  half8_t o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float g = (float)gh[e];
+    o[e] = (half_t)(g / (1.0f + expf(-g))) * uh[e];
+  }
+  return __builtin_bit_cast(uint4_t, o);
+}
+
+template <int NB, int MM, WFmt F, XMode XM = XMode::Plain>
+__global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ? flat_min_waves<NB, F>() : 1)) void gemv_flat_kernel(
     const half_t* __restrict__ x, int M, int K, const void* __restrict__ wsrc, const void* __restrict__ wmeta,
-    const half_t* __restrict__ bias, int N, int g_shift, half_t* __restrict__ y, int S,
-    float4_t* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt) {
+    const half_t* __restrict__ bias, int N, int g_shift, half_t* y, int S,
+    float4_t* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt, FuseArgs fz) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int NBX = NB + 1;                                // staged slice length (blocks)
   constexpr int D = NB <= 3 ? NB : ((NB + 1) / 2 < 3 ? 3 : (NB + 1) / 2);   // weight blocks in flight
@@ -322,14 +368,28 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
   half_t* xl = reinterpret_cast<half_t*>(wl);
   uint8_t* ml = wl + kXBytes;
 
-  // 1) x slice (and the W4 records): small, mostly L2 hits.
+  // 1) x slice (and the W4 records): small, mostly L2 hits.  The fused
+  //    modes (M = 1 only) also fetch what they transform x with: RmsNorm the
+  //    norm weight and the producer's per-tile sums of squares, SiluMul the
+  //    up half of a [2K] x.  The transform itself waits until the weight
+  //    loads below are in flight.
   uint4_t xr[kXPerLane];
+  uint4_t xa[XM == XMode::Plain ? 1 : kXPerLane];   // up half (SiluMul) or norm weight (RmsNorm)
+  constexpr int kSqPerLane = 8;                     // sums of squares held per lane before the weights
+  float sq[XM == XMode::RmsNorm ? kSqPerLane : 1];
+  auto x_offset = [&](int j) { return min(b0 * kW4BlockK + (min(lane + 64 * j, kXChunks - 1) % (NBX * 16)) * 8, K - 8); };
 #pragma unroll
   for (int j = 0; j < kXPerLane; ++j) {
-    const int c = min(lane + 64 * j, kXChunks - 1);
-    const int m = min(c / (NBX * 16), M - 1);
-    const int off = min(b0 * kW4BlockK + (c % (NBX * 16)) * 8, K - 8);
+    const int m = min(min(lane + 64 * j, kXChunks - 1) / (NBX * 16), M - 1);
+    const int off = x_offset(j);
     xr[j] = *reinterpret_cast<const uint4_t*>(x + (size_t)m * K + off);
+    if constexpr (XM == XMode::SiluMul) xa[j] = *reinterpret_cast<const uint4_t*>(x + K + off);
+    if constexpr (XM == XMode::RmsNorm) xa[j] = *reinterpret_cast<const uint4_t*>(fz.norm_w + off);
+  }
+  if constexpr (XM == XMode::RmsNorm) {
+    // Unconditional (clamped) loads; entries past the count are dropped when summed.
+#pragma unroll
+    for (int u = 0; u < kSqPerLane; ++u) sq[u] = fz.sumsq_in[min(lane + 64 * u, fz.sumsq_count - 1)];
   }
   int g_lo = 0;
   uint2_t mr[kMPerLane > 0 ? kMPerLane : 1];
@@ -367,8 +427,21 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
   for (int s2 = 0; s2 < D; ++s2) load_block(ring[s2], s2);
   if (more) load_block(xtra, NB);
 
-  // 3) park x and the records in this wave's LDS region (every lane stores,
-  //    so the loads above stay ahead of the weight loads).
+  // 3) transform x for the fused modes, then park x and the records in this
+  //    wave's LDS region (every lane stores, so the loads above stay ahead of
+  //    the weight loads).
+  if constexpr (XM == XMode::SiluMul) {
+#pragma unroll
+    for (int j = 0; j < kXPerLane; ++j) xr[j] = silu_mul8(xr[j], xa[j]);
+  }
+  if constexpr (XM == XMode::RmsNorm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < kSqPerLane; ++u) ss += lane + 64 * u < fz.sumsq_count ? sq[u] : 0.f;
+    const float r = rsqrtf(wave_sum_f(ss) / (float)K + fz.eps);
+#pragma unroll
+    for (int j = 0; j < kXPerLane; ++j) xr[j] = rms_scale8(xr[j], xa[j], r);
+  }
 #pragma unroll
   for (int j = 0; j < kXPerLane; ++j)
     reinterpret_cast<uint4_t*>(xl)[lane + 64 * j] = F == WFmt::W4 ? w4_prescale_x(xr[j]) : xr[j];
@@ -454,11 +527,25 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
   if (has_x) {
     const int n0 = tile * 16 + 4 * kb;
     if constexpr (F == WFmt::W4) {
-      if (n0 < N) {
-        half4_t o;
+      half4_t o;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = (half_t)sum[v];
+      for (int v = 0; v < 4; ++v) o[v] = (half_t)sum[v];
+      if (n0 < N) {
+        // Fused residual (M = 1): y = residual + fp16(x.W^T), as the
+        // reference adds the rounded projection to the fp16 residual.
+        if (fz.residual) o = *reinterpret_cast<const half4_t*>(fz.residual + n0) + o;
         *reinterpret_cast<half4_t*>(y + (size_t)i * N + n0) = o;
+      }
+      if (fz.sumsq_out) {
+        // Lanes 0, 16, 32, 48 hold the tile's 16 outputs (M = 1).
+        float q = 0.f;
+        if (n0 < N) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) q += (float)o[v] * (float)o[v];
+        }
+        q += __shfl_xor(q, 16);
+        q += __shfl_xor(q, 32);
+        if (lane == 0) fz.sumsq_out[tile] = q;
       }
     } else {
       const half_t* scale = reinterpret_cast<const half_t*>(wmeta);
@@ -631,9 +718,9 @@ size_t flat_workspace_bytes(int ntile, int split) {
   return (((size_t)ntile * 4 + 255) & ~(size_t)255) + (size_t)ntile * split * 64 * sizeof(float4_t);
 }
 
-template <int NB, int MM, WFmt F>
+template <int NB, int MM, WFmt F, XMode XM>
 int launch_flat(const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias, int N,
-                int g_shift, half_t* y, FlatPlan p, void* ws, hipStream_t s) {
+                int g_shift, half_t* y, FlatPlan p, void* ws, const FuseArgs& fz, hipStream_t s) {
   if (p.ksw > flat_max_ksw<NB, F>()) return kNotApplicable;
   const int lds = flat_lds_bytes<NB, MM, F>(p.ksw);
   if (lds > kGemvMaxBytes) return kNotApplicable;
@@ -642,25 +729,26 @@ int launch_flat(const half_t* x, int M, int K, const void* w, const void* meta, 
   float4_t* part = p.split > 1 ? reinterpret_cast<float4_t*>(reinterpret_cast<uint8_t*>(ws) +
                                                              (((size_t)ntile * 4 + 255) & ~(size_t)255))
                                : nullptr;
-  hipLaunchKernelGGL((gemv_flat_kernel<NB, MM, F>), dim3((unsigned)ntile, (unsigned)p.split), dim3(64 * p.ksw), lds,
-                     s, x, M, K, w, meta, bias, N, g_shift, y, p.split, part, cnt);
+  hipLaunchKernelGGL((gemv_flat_kernel<NB, MM, F, XM>), dim3((unsigned)ntile, (unsigned)p.split), dim3(64 * p.ksw),
+                     lds, s, x, M, K, w, meta, bias, N, g_shift, y, p.split, part, cnt, fz);
   return check_launch(F == WFmt::W4 ? "w4_gemv_flat" : "w8_gemv_flat");
 }
 
-template <int MM, WFmt F, int NB = 1>
+template <int MM, WFmt F, XMode XM, int NB = 1>
 int launch_flat_nb(int nb, const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias,
-                   int N, int g_shift, half_t* y, FlatPlan p, void* ws, hipStream_t s) {
+                   int N, int g_shift, half_t* y, FlatPlan p, void* ws, const FuseArgs& fz, hipStream_t s) {
   if constexpr (NB > kFlatMaxNB) {
     return kNotApplicable;
   } else {
-    if (nb == NB) return launch_flat<NB, MM, F>(x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
-    return launch_flat_nb<MM, F, NB + 1>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
+    if (nb == NB) return launch_flat<NB, MM, F, XM>(x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
+    return launch_flat_nb<MM, F, XM, NB + 1>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
   }
 }
 
 template <WFmt F>
 int launch_gemv_flat(const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias, int N,
-                     int g_shift, half_t* y, void* ws, size_t ws_bytes, hipStream_t s) {
+                     int g_shift, half_t* y, void* ws, size_t ws_bytes, hipStream_t s,
+                     XMode xm = XMode::Plain, const FuseArgs& fz = FuseArgs{}) {
   const int nblk = K / kW4BlockK, ntile = (N + 15) / 16;
   FlatPlan p = plan_flat<F>(ntile, nblk);
   // Without enough workspace the tile's k range stays in one workgroup.
@@ -668,8 +756,12 @@ int launch_gemv_flat(const half_t* x, int M, int K, const void* w, const void* m
     p = plan_flat<F>(ntile, nblk, false);
   const int nb = (nblk / p.split) / p.ksw;
   if (nb < 1 || nb > kFlatMaxNB) return kNotApplicable;
-  if (M == 1) return launch_flat_nb<1, F>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
-  return launch_flat_nb<4, F>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, s);
+  if constexpr (F == WFmt::W4) {
+    if (xm == XMode::RmsNorm) return launch_flat_nb<1, F, XMode::RmsNorm>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
+    if (xm == XMode::SiluMul) return launch_flat_nb<1, F, XMode::SiluMul>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
+  }
+  if (M == 1) return launch_flat_nb<1, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
+  return launch_flat_nb<4, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
 }
 
 int launch_w4_gemv_flat(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
@@ -680,6 +772,21 @@ int launch_w4_gemv_flat(const half_t* x, int M, int K, const uint4_t* tiles, con
 }
 
 }  // namespace
+
+int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
+                         int x_mode, const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
+                         const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
+                         hipStream_t s) {
+  const int bpg = G / kW4BlockK;
+  if (bpg & (bpg - 1)) return fail(WQ_ERR_UNSUPPORTED, "fused decode linear needs group size 128 * 2^j");
+  const FuseArgs fz{norm_w, sumsq_in, sumsq_count, eps, residual, sumsq_out};
+  const XMode xm = x_mode == 1 ? XMode::RmsNorm : x_mode == 2 ? XMode::SiluMul : XMode::Plain;
+  const int rc = launch_gemv_flat<WFmt::W4>(x, 1, K, tiles, meta, nullptr, N, __builtin_ctz(bpg), y, ws, ws_bytes, s,
+                                            xm, fz);
+  if (rc == kNotApplicable)
+    return fail(WQ_ERR_UNSUPPORTED, "fused decode linear: this k is beyond the decode kernel's blocks per wave");
+  return rc;
+}
 
 size_t gemv_workspace_bytes(bool w4, int64_t m, int64_t n, int64_t k) {
   if (m > kGemvFlatMaxM) return 0;

@@ -165,12 +165,14 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
 
 class DecodeStepGraph:
     """One batch-1 decode token of the whole model, captured once as a HIP
-    graph over model-owned buffers: embedding row -> 40 x [add+RMSNorm, fused
-    QKV linear, attention (q/k norm, RoPE, KV append, GQA softmax), o linear,
-    add+RMSNorm, fused gate_up linear, SiLU*up, down linear] -> final norm ->
-    fp16 LM head.  Inputs are the token id and the position (device
-    scalars); every launch is a HIP kernel of this library except the
-    embedding gather and the fp16 LM-head GEMM (torch)."""
+    graph over model-owned buffers: embedding row -> per layer [fused QKV
+    linear (RMSNorm in its prologue), attention (q/k norm, RoPE, KV append,
+    GQA softmax, chunk merge), o linear (+ residual), fused gate_up linear
+    (RMSNorm prologue), down linear (SiLU*up prologue, + residual)] -> final
+    norm -> fp16 LM head.  W8 weights take the same steps with the norms,
+    residual adds and SiLU*up as separate kernels.  Inputs are the token id
+    and the position (device scalars); every launch is a HIP kernel of this
+    library except the embedding gather and the fp16 LM-head GEMM (torch)."""
 
     def __init__(self, model: 'QuantizedQwen3ForCausalLM', key_cache: list[Tensor], value_cache: list[Tensor],
                  max_seq_len: int):
@@ -204,6 +206,12 @@ class DecodeStepGraph:
                     raise ValueError(f'decode graph needs prepared {name}')
         self.embed = model.device_embedding()
         self.lm_head_t = model.lm_head.t()
+        from .weight_quantization.backend import PreparedW4
+        names = ('self_attn.qkv_proj', 'self_attn.o_proj', 'mlp.gate_up_proj', 'mlp.down_proj')
+        self.fused = all(isinstance(w[p + '._prepared'], PreparedW4) for w in self.layers for p in names) and \
+            hidden % 16 == 0
+        self.sumsq_o = torch.zeros(hidden // 16, dtype=torch.float32, device=dev)
+        self.sumsq_down = torch.zeros(hidden // 16, dtype=torch.float32, device=dev)
         # One eager step loads every code object and the GEMM's handles, then
         # the capture (the eager step's KV row 0 is rewritten by any prefill).
         self._step()
@@ -219,6 +227,47 @@ class DecodeStepGraph:
         self.model.linear_backend._fused(x, prepared, out)
 
     def _step(self) -> None:
+        if self.fused:
+            self._step_fused()
+        else:
+            self._step_unfused()
+
+    def _step_fused(self) -> None:
+        """W4 weights: the RMSNorms, residual adds and SiLU*up ride inside the
+        decode linears (wq_w4a16_decode_fused): per layer one QKV linear, the
+        attention, and the o, gate_up and down linears."""
+        cfg = self.model.config
+        eps = cfg.rms_norm_eps
+        nat = _native
+        torch.index_select(self.embed, 0, self.token, out=self.hidden)
+        hid = self.hidden.view(-1)
+        for idx, w in enumerate(self.layers):
+            qkv_p, o_p = w[QKV_FUSED.removesuffix('.weight') + '._prepared'], w['self_attn.o_proj._prepared']
+            gu_p, dn_p = w[GATE_UP_FUSED.removesuffix('.weight') + '._prepared'], w['mlp.down_proj._prepared']
+            if idx == 0:
+                nat.add_rmsnorm(self.hidden, w['input_layernorm.weight'], eps, out=self.states)
+                nat.w4a16_decode_fused(self.states.view(-1), qkv_p.tiles, qkv_p.meta, qkv_p.n, qkv_p.group_size,
+                                       out=self.qkv, workspace=qkv_p.workspace)
+            else:
+                nat.w4a16_decode_fused(hid, qkv_p.tiles, qkv_p.meta, qkv_p.n, qkv_p.group_size,
+                                       x_mode=nat.X_RMSNORM, norm_weight=w['input_layernorm.weight'],
+                                       sumsq_in=self.sumsq_down, eps=eps, out=self.qkv, workspace=qkv_p.workspace)
+            nat.decode_attention(self.qkv.view(-1), cfg.num_attention_heads, cfg.num_key_value_heads,
+                                 w['self_attn.q_norm.weight'], w['self_attn.k_norm.weight'], eps, self.cos,
+                                 self.sin, self.position, self.kc[idx], self.vc[idx], self.scale, out=self.attn,
+                                 workspace=self.attn_ws)
+            nat.w4a16_decode_fused(self.attn, o_p.tiles, o_p.meta, o_p.n, o_p.group_size, residual=hid,
+                                   sumsq_out=self.sumsq_o, out=hid, workspace=o_p.workspace)
+            nat.w4a16_decode_fused(hid, gu_p.tiles, gu_p.meta, gu_p.n, gu_p.group_size, x_mode=nat.X_RMSNORM,
+                                   norm_weight=w['post_attention_layernorm.weight'], sumsq_in=self.sumsq_o, eps=eps,
+                                   out=self.gate_up, workspace=gu_p.workspace)
+            nat.w4a16_decode_fused(self.gate_up.view(-1), dn_p.tiles, dn_p.meta, dn_p.n, dn_p.group_size,
+                                   x_mode=nat.X_SILU_MUL, residual=hid, sumsq_out=self.sumsq_down, out=hid,
+                                   workspace=dn_p.workspace)
+        nat.add_rmsnorm(self.hidden, self.model.final_norm, eps, out=self.states)
+        torch.mm(self.states, self.lm_head_t, out=self.logits)
+
+    def _step_unfused(self) -> None:
         cfg = self.model.config
         eps = cfg.rms_norm_eps
         torch.index_select(self.embed, 0, self.token, out=self.hidden)
@@ -305,7 +354,8 @@ class QuantizedQwen3ForCausalLM:
             entry = {'k': [torch.zeros(shape, device=dev, dtype=self.dtype) for _ in range(cfg.num_hidden_layers)],
                      'v': [torch.zeros(shape, device=dev, dtype=self.dtype) for _ in range(cfg.num_hidden_layers)],
                      'graph': None}
-            if self.decode_graph_enabled and batch_size == 1 and dev.type == 'cuda':
+            if self.decode_graph_enabled and batch_size == 1 and dev.type == 'cuda' and \
+                    max_seq_len <= _native.DECODE_ATTENTION_MAX_SEQ:
                 entry['graph'] = DecodeStepGraph(self, entry['k'], entry['v'], max_seq_len)
             entries.append(entry)
         entry['owner'] = weakref.ref(cache)

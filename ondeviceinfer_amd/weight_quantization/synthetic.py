@@ -67,9 +67,11 @@ def random_compressed_store(cfg: Qwen3Config, *, seed: int = 0, device: str | to
             size = cfg.head_dim if 'q_norm' in name or 'k_norm' in name else cfg.hidden_size
             layer[name] = (1.0 + 0.1 * torch.randn(size, device=device, generator=gen)).half()
         layers.append(layer)
-    embed = (torch.randn(cfg.vocab_size, cfg.hidden_size, generator=cpu_gen) * 0.02).half()
+    # Drawn on `device` (fast for the 151936 x 5120 tables), kept on the host.
+    big = gen if device.type == 'cuda' else cpu_gen
+    embed = (torch.randn(cfg.vocab_size, cfg.hidden_size, device=device, generator=big) * 0.02).half().cpu()
     lm_head = embed if cfg.tie_word_embeddings else \
-        (torch.randn(cfg.vocab_size, cfg.hidden_size, generator=cpu_gen) * 0.02).half()
+        (torch.randn(cfg.vocab_size, cfg.hidden_size, device=device, generator=big) * 0.02).half().cpu()
     final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden_size, generator=cpu_gen)).half()
     manifest = {'source': 'synthetic', 'seed': seed, 'quantization_config': quantization_config(group_size, symmetric)}
     return CompressedStore(cfg, layers, embed, final_norm, lm_head, manifest)

@@ -129,14 +129,16 @@ def _status(fn, *args):
 def test_decode_op_argument_checks_on_the_host():
     b = ctypes.c_size_t()
     assert _status('wq_decode_attention_workspace_size', 40, 8, 128, 4224, ctypes.byref(b)) == _native.WQ_OK
-    ml = (8 * 66 * 5 * 2 * 4 + 255) // 256 * 256          # counters | (max, sum) | partial outputs
-    assert b.value == 256 + ml + 8 * 66 * 5 * 128 * 4
+    # 66 sub-chunks of 64 positions -> 33 workgroups of 2 per kv head
+    ml = (8 * 33 * 5 * 2 * 4 + 255) // 256 * 256          # (max, sum) | partial outputs
+    assert b.value == ml + 8 * 33 * 5 * 128 * 4
     assert _status('wq_decode_attention_workspace_size', 40, 8, 64, 4224, ctypes.byref(b)) == _native.WQ_ERR_UNSUPPORTED
     assert b'head_dim 128' in _native.load().wq_last_error()
     assert _status('wq_decode_attention_workspace_size', 40, 3, 128, 4224, ctypes.byref(b)) == \
         _native.WQ_ERR_INVALID_ARGUMENT
     assert _status('wq_decode_attention_workspace_size', 80, 8, 128, 64, ctypes.byref(b)) == _native.WQ_ERR_UNSUPPORTED
-    assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 1 << 20, ctypes.byref(b)) == \
+    assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 8192, ctypes.byref(b)) == _native.WQ_OK
+    assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 8193, ctypes.byref(b)) == \
         _native.WQ_ERR_UNSUPPORTED
     assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 64, ctypes.byref(b)) == _native.WQ_OK
     assert b.value == 0        # one chunk: no cross-workgroup merge
