@@ -51,10 +51,6 @@ LAYER_SHAPES = [  # (name, K, N) in decoder order
     ('self_attn.o_proj', HIDDEN, HIDDEN), ('mlp.gate_proj', HIDDEN, INTER), ('mlp.up_proj', HIDDEN, INTER),
     ('mlp.down_proj', INTER, HIDDEN),
 ]
-STEP_LINEARS = [  # the four linears of the decode step (fused where the model fuses)
-    ('self_attn.qkv_proj', HIDDEN, QKV), ('self_attn.o_proj', HIDDEN, HIDDEN),
-    ('mlp.gate_up_proj', HIDDEN, GATE_UP), ('mlp.down_proj', INTER, HIDDEN),
-]
 
 
 def w4_bytes(m: int, n: int, k: int, g: int = GROUP) -> int:
@@ -95,14 +91,15 @@ def flat_plan(n: int, k: int) -> tuple[int, int, int]:
     return split, ksw, per // ksw
 
 
-def kernel_name_for(native_shape: tuple[int, int, int]) -> str:
+def kernel_name_for(native_shape: tuple[int, int, int], mode: str = 'Plain') -> str:
     """Kernel the library runs for (M, N, K): M <= 4 goes to the decode GEMV
-    gemv_flat_kernel<NB, MM, W4> (NB = k blocks per wave, MM = 1 or 4)."""
+    gemv_flat_kernel<NB, MM, W4[, mode]> (NB = k blocks per wave, MM = 1 or 4;
+    mode = the fused x transform of wq_w4a16_decode_fused)."""
     m, n, k = native_shape
     if m > 4:
         return 'w4_skinny_kernel' if m <= 64 else 'wq_gemm_kernel'
     _, _, nb = flat_plan(n, k)
-    return f'gemv_flat_kernel<{nb}, {1 if m == 1 else 4}, W4>'
+    return f'gemv_flat_kernel<{nb}, {1 if m == 1 else 4}, W4' + ('' if mode == 'Plain' else f', {mode}') + '>'
 
 
 def profiled_traffic(kernel: str, shape: str):
@@ -280,11 +277,50 @@ def main() -> int:
                                'pct_hbm_peak': round(100.0 * pass_bytes / sec / 1e9 / HBM_PEAK_GBS, 2),
                                'us_per_pass': round(sec * 1e6, 1), 'bytes_per_pass': pass_bytes}
 
-        # Kernels of the decode step, each as a graph of its `layers` launches.
+        # Kernels of the decode step as the step issues them (fused prologues
+        # and epilogues, one weight set per layer), each as a graph of its
+        # `layers` launches; then the plain per-projection GEMVs beside them.
         kernels = []
-        step_ops = {s[0] for s in STEP_LINEARS}
-        extra = [s for s in LAYER_SHAPES if s[0] in ('self_attn.q_proj', 'self_attn.k_proj', 'mlp.gate_proj')]
-        for name, k, n in STEP_LINEARS + extra:
+        eps = cfg.rms_norm_eps
+        hid = torch.randn(HIDDEN, device=device).half()
+        res = torch.randn(HIDDEN, device=device).half()
+        gu_in = torch.randn(GATE_UP, device=device).half()
+        att_in = torch.randn(HIDDEN, device=device).half()
+        norm_w = (1.0 + 0.1 * torch.randn(HIDDEN, device=device)).half()
+        sumsq_in = (hid.float() ** 2).view(-1, 16).sum(1).contiguous()   # per-16-row sums, as a producer writes
+        sumsq_out = torch.empty(HIDDEN // 16, device=device)
+        step_calls = [  # (op, K, N, kernel mode, fused-call keywords)
+            ('self_attn.qkv_proj', HIDDEN, QKV, 'RmsNorm',
+             dict(x=hid, x_mode=native.X_RMSNORM, norm_weight=norm_w, sumsq_in=sumsq_in, eps=eps)),
+            ('self_attn.o_proj', HIDDEN, HIDDEN, 'Plain', dict(x=att_in, residual=res, sumsq_out=sumsq_out)),
+            ('mlp.gate_up_proj', HIDDEN, GATE_UP, 'RmsNorm',
+             dict(x=hid, x_mode=native.X_RMSNORM, norm_weight=norm_w, sumsq_in=sumsq_in, eps=eps)),
+            ('mlp.down_proj', INTER, HIDDEN, 'SiluMul',
+             dict(x=gu_in, x_mode=native.X_SILU_MUL, residual=res, sumsq_out=sumsq_out)),
+        ]
+        for name, k, n, mode, kw in step_calls:
+            y = torch.empty(1, n, device=device, dtype=torch.float16)
+            extra_kw = {a: v for a, v in kw.items() if a != 'x'}
+
+            def fused_pass():
+                for w in layers:
+                    p = w[name + '._prepared']
+                    native.w4a16_decode_fused(kw['x'], p.tiles, p.meta, p.n, GROUP, out=y, workspace=p.workspace,
+                                              **extra_kw)
+            fused_pass()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fused_pass()
+            per = time_graph(torch, g, 10) / len(layers)
+            b = w4_bytes(1, n, k) + (2 * k if mode == 'SiluMul' else 0) + (2 * n if 'residual' in kw else 0)
+            kernels.append({'op': name, 'fusion': mode + (' + residual + sumsq' if 'residual' in kw else ''),
+                            'shape': f'{k}->{n}', 'kernel': kernel_name_for((1, n, k), mode), 'bytes': b,
+                            'us_per_launch': round(per * 1e6, 3), 'gbs': round(b / per / 1e9, 1),
+                            'frac': round(b / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': True,
+                            'launches_per_token': args.layers})
+            del g, y
+        for name, k, n in [s for s in LAYER_SHAPES if s[0] in ('self_attn.q_proj', 'self_attn.k_proj',
+                                                                  'mlp.gate_proj', 'mlp.down_proj')]:
             y = torch.empty(1, n, device=device, dtype=torch.float16)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
@@ -292,33 +328,37 @@ def main() -> int:
                     linear(xs[k], w[name + '._prepared'], y)
             per = time_graph(torch, g, 10) / len(layers)
             b = w4_bytes(1, n, k)
-            kernels.append({'op': name, 'shape': f'{k}->{n}', 'kernel': kernel_name_for((1, n, k)), 'bytes': b,
+            kernels.append({'op': name, 'fusion': 'none (unfused projection)', 'shape': f'{k}->{n}',
+                            'kernel': kernel_name_for((1, n, k)), 'bytes': b,
                             'us_per_launch': round(per * 1e6, 3), 'gbs': round(b / per / 1e9, 1),
-                            'frac': round(b / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': name in step_ops,
+                            'frac': round(b / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': False,
                             'launches_per_token': args.layers})
             del g, y
-        # the attention kernel at the decode position of the timed steps
-        kc = [torch.randn(cfg.num_key_value_heads, capacity, 128, device=device).half() for _ in range(2)]
+        # Attention (+ chunk merge) at the decode position of the timed steps,
+        # one KV cache per layer as in the step.
+        kvh = cfg.num_key_value_heads
+        kc = [[torch.randn(kvh, capacity, 128, device=device).half() for _ in range(2)] for _ in range(args.layers)]
         qkv = torch.randn(QKV, device=device).half()
         cos, sin = model.rotary_emb.table(capacity, device)
         pos = torch.tensor([PROMPT + args.warmup], dtype=torch.int32, device=device)
         att_out = torch.empty(HIDDEN, device=device, dtype=torch.float16)
-        ws = torch.zeros(native.decode_attention_workspace_size(40, 8, 128, capacity), dtype=torch.uint8,
-                         device=device)
+        ws = torch.empty(native.decode_attention_workspace_size(cfg.num_attention_heads, kvh, 128, capacity),
+                         dtype=torch.uint8, device=device)
         qn = torch.ones(128, device=device).half()
 
-        def attn():
-            native.decode_attention(qkv, 40, 8, qn, qn, 1e-6, cos, sin, pos, kc[0], kc[1], 128 ** -0.5,
-                                    out=att_out, workspace=ws)
-        attn()
+        def attn_pass():
+            for c in kc:
+                native.decode_attention(qkv, cfg.num_attention_heads, kvh, qn, qn, eps, cos, sin, pos, c[0], c[1],
+                                        128 ** -0.5, out=att_out, workspace=ws)
+        attn_pass()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for _ in range(args.layers):
-                attn()
+            attn_pass()
         per = time_graph(torch, g, 10) / args.layers
-        att_bytes = 2 * 8 * (PROMPT + args.warmup) * 128 * 2 + QKV * 2 + HIDDEN * 2
-        kernels.append({'op': 'attention', 'shape': f'GQA 40/8 x 128, {PROMPT + args.warmup + 1} keys',
-                        'kernel': 'decode_attention_kernel', 'bytes': att_bytes,
+        att_bytes = 2 * kvh * (PROMPT + args.warmup) * 128 * 2 + QKV * 2 + HIDDEN * 2
+        kernels.append({'op': 'attention', 'fusion': 'q/k RMSNorm + RoPE + cache append; chunk-merge launch',
+                        'shape': f'GQA {cfg.num_attention_heads}/{kvh} x 128, {PROMPT + args.warmup + 1} keys',
+                        'kernel': 'decode_attention_kernel + decode_attention_merge_kernel', 'bytes': att_bytes,
                         'us_per_launch': round(per * 1e6, 3), 'gbs': round(att_bytes / per / 1e9, 1),
                         'frac': round(att_bytes / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': True,
                         'launches_per_token': args.layers})

@@ -21,6 +21,7 @@ typedef _Float16 half_t;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
@@ -184,6 +185,19 @@ __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
 
 __device__ __forceinline__ half8_t ld_h8(const half_t* p) {
   return *reinterpret_cast<const half8_t*>(p);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x on the transcendental unit (v_exp_f32, about 1 ulp; -inf -> 0).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// silu(g) = g / (1 + e^-g) as g * rcp(1 + 2^(-g log2 e)): two transcendental
+// ops instead of expf and an IEEE divide.  The fp32 result is within a few
+// ulp of the exact quotient, far below the fp16 rounding that follows it;
+// g -> -inf gives -0 (rcp(inf) = 0), g -> +inf gives g.
+__device__ __forceinline__ float silu_f(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + exp2_hw(-g * kLog2e));
 }
 
 }  // namespace wq

@@ -109,32 +109,28 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const half_t* __restrict_
     const half8_t u = ld_h8(gu + r * 2 * n + n + 8 * c);
     half8_t o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float gf = (float)g[e];
-      o[e] = (half_t)(gf / (1.0f + expf(-gf))) * u[e];
-    }
+    for (int e = 0; e < 8; ++e) o[e] = (half_t)silu_f((float)g[e]) * u[e];
     *reinterpret_cast<half8_t*>(out + r * n + 8 * c) = o;
   }
 }
 
 // ---------------------------------------------------------------- attention
 // Per-head RMSNorm and RoPE of one 128-vector held two elements per lane
-// (lane l: elements 2l, 2l+1).  rotate_half pairs element d with d +- 64,
-// i.e. lane l with lane l ^ 32.  Every product and the sum round to fp16, as
-// in `q * cos + rotate_half(q) * sin` on fp16 tensors.
-__device__ __forceinline__ half2_t norm_rope_pair(half2_t v, const half_t* nw, float eps, const half_t* cs,
-                                                  const half_t* sn, int lane) {
+// (lane l: elements 2l, 2l+1), with the lane's norm weights, cos and sin
+// already loaded.  rotate_half pairs element d with d +- 64, i.e. lane l
+// with lane l ^ 32.  Every product and the sum round to fp16, as in
+// `q * cos + rotate_half(q) * sin` on fp16 tensors.
+__device__ __forceinline__ half2_t norm_rope_pair(half2_t v, bool norm, half2_t nw, float eps, half2_t c2,
+                                                  half2_t s2, int lane) {
 #pragma clang fp contract(off)
-  if (nw) {
+  if (norm) {
     const float a = (float)v[0], b = (float)v[1];
     const float r = rsqrtf(wave_sum(a * a + b * b) * (1.0f / kHeadDim) + eps);
-    v[0] = nw[2 * lane] * (half_t)(a * r);
-    v[1] = nw[2 * lane + 1] * (half_t)(b * r);
+    v[0] = nw[0] * (half_t)(a * r);
+    v[1] = nw[1] * (half_t)(b * r);
   }
   half2_t p = as_h2(__shfl_xor(as_u32(v), 32));
   if (lane < 32) p = -p;
-  const half2_t c2 = {cs[2 * lane], cs[2 * lane + 1]};
-  const half2_t s2 = {sn[2 * lane], sn[2 * lane + 1]};
   const half2_t t1 = v * c2;
   const half2_t t2 = p * s2;
   return t1 + t2;
@@ -153,253 +149,288 @@ AttnSplit attn_split(int64_t max_seq) {
   return {spc, (int)((subs + spc - 1) / spc)};
 }
 
+// Orders this wave's LDS accesses around a wave-private exchange (the
+// compiler reasons per lane and could otherwise move a lane's read of another
+// lane's value above the write; the hardware keeps one wave's LDS operations
+// in order).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // grid = (kv_heads, chunks); 256 threads = 4 waves.  Workgroup c of kv head
-// h covers positions [c * SPC * 64, (c + 1) * SPC * 64) in sub-chunks of 64,
-// with an online softmax over the head's G <= 8 query heads:
-//   loads   every K fragment and V row this workgroup needs is requested
-//           before the q/k prologue (rows clamped into the cache; rows past
-//           L or at `pos` are replaced below);
-//   scores  S[g][p] = q_g . k_p on the matrix cores: A = the query heads
-//           (rows g, zero past G), B = 16 key rows per wave (each lane 16
-//           bytes of one row), four k-steps of 32 elements;
-//   softmax DPP row r (16 lanes x 4 positions) of wave w owns query head
-//           4w + r: running max / sum and the rescale factor;
-//   P.V     lane (dg, q) of wave w: elements 8dg .. 8dg+7 of positions
-//           4(q + 4w) .. +3, one 16-byte V load per position, one float4
-//           of P per head; the four position quads of a wave are summed
-//           with shuffles at the end.
-// The workgroup whose chunk holds `pos` also normalizes, rotates and
-// appends the new key and value, and takes them from LDS.  With one chunk
-// per head the workgroup writes the output; otherwise each chunk writes its
-// (max, sum, unnormalized output) to the workspace and
-// decode_attention_merge_kernel, launched next, combines them.
+// h covers positions [c * SPC * 64, (c + 1) * SPC * 64); in each sub-chunk of
+// 64 positions wave w owns positions 16w .. 16w + 15 and runs its own online
+// softmax over them for the head's G <= 8 query heads, so the sub-chunk loop
+// has no workgroup barrier.  Lane l is (r, i) = (l / 16, l % 16).
+//   loads   the prologue's operands (q, cos/sin rows, norm weights, the new
+//           k/v) are requested first, then every K fragment and V row this
+//           workgroup needs (rows clamped into the cache; rows past L or at
+//           `pos` are replaced below), so the q/k prologue runs while the
+//           cache streams in;
+//   scores  S[g][p] = q_g . k_p on the matrix cores (16x16x32): A = the query
+//           heads (rows g, zero past G), B = the wave's 16 key rows (each
+//           lane 16 bytes of one row); lane (r, i) gets heads 4r .. 4r+3 at
+//           position i, in log2 units (scale * log2 e);
+//   softmax the 16 lanes of DPP row r reduce max and sum for heads 4r + v;
+//   P.V     on the matrix cores (16x16x16): A = P as fp16 [head][position],
+//           B = V^T [d][position], both through wave-private LDS (the V rows
+//           arrive 16 bytes of d per lane and are written transposed), one
+//           MFMA per 16 values of d; the accumulator rows are the heads 4r+v
+//           of the lane's own softmax row, so the online rescale is local.
+// At the end the four waves' (max, sum, output) are combined through LDS.
+// The workgroup whose chunk holds `pos` also normalizes, rotates and appends
+// the new key and value and takes them from LDS.  With one chunk per head
+// the workgroup writes the output; otherwise every chunk, active or not,
+// writes its (max, sum) pair and unnormalized output to the workspace, and
+// decode_attention_merge_kernel (the next launch) combines them without
+// reading the position: an empty chunk writes (-inf, 0) and zeros and weighs
+// nothing, and an invalid position leaves every max at -inf, which the merge
+// turns into NaN.
 template <int G, int SPC>
 __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
     const half_t* __restrict__ qkv, int H, int KV, const half_t* __restrict__ qn_w,
     const half_t* __restrict__ kn_w, float eps, const half_t* __restrict__ cos_t, const half_t* __restrict__ sin_t,
-    const int32_t* __restrict__ position, half_t* kc, half_t* vc, int max_seq, float scale,
+    const int32_t* __restrict__ position, half_t* kc, half_t* vc, int max_seq, float scale_log2,
     half_t* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   constexpr int D = kHeadDim, C = kSub, GM = kMaxGroup;
+  constexpr int VTS = 20;   // V^T row stride in halves (40 bytes: the 16 B-fragment reads hit distinct banks)
   __shared__ __attribute__((aligned(16))) half_t qh[GM][D];
   __shared__ __attribute__((aligned(16))) half_t knew[D];
   __shared__ __attribute__((aligned(16))) half_t vnew[D];
-  __shared__ __attribute__((aligned(16))) float sc[GM][C];
-  __shared__ float alph[GM];
-  __shared__ __attribute__((aligned(16))) float red[4 * GM * D];   // per-wave P.V partials; later the merge's staging
-  __shared__ float mls[GM][2];
+  __shared__ __attribute__((aligned(16))) half_t pl[4][16][16];    // per-wave P, [head][position]
+  __shared__ __attribute__((aligned(16))) half_t vt[4][D][VTS];    // per-wave V^T, [d][position]
+  __shared__ __attribute__((aligned(16))) float red[4][GM][D];    // per-wave unnormalized outputs
+  __shared__ float mlw[4][GM][2];                                 // per-wave (max, sum)
 
   const int h = blockIdx.x, chunk = blockIdx.y, NC = gridDim.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i = lane & 15, kb = lane >> 4;
   const int pos = *position;
-  if (pos < 0 || pos >= max_seq) {
-    if (h == 0 && chunk == 0)
-      for (int j = tid; j < H * D; j += 256) out[j] = (half_t)__builtin_nanf("");
+  const bool valid = pos >= 0 && pos < max_seq;
+  const int L = valid ? pos + 1 : 0;
+  const int p0 = chunk * SPC * C;
+  if (p0 >= L) {
+    // Nothing to attend in this chunk (every chunk, when the position is
+    // invalid; chunk 0 is active whenever it is valid).
+    if (NC == 1) {
+      for (int j = tid; j < G * D; j += 256) out[(size_t)h * G * D + j] = (half_t)__builtin_nanf("");
+    } else {
+      for (int j = tid; j < G * (D / 4); j += 256) {
+        const size_t slot = (size_t)(h * G + j / (D / 4)) * NC + chunk;
+        *reinterpret_cast<float4_t*>(ws_o + slot * D + 4 * (j % (D / 4))) = float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      if (tid < G) {
+        ws_ml[((size_t)(h * G + tid) * NC + chunk) * 2] = -INFINITY;
+        ws_ml[((size_t)(h * G + tid) * NC + chunk) * 2 + 1] = 0.f;
+      }
+    }
     return;
   }
-  const int L = pos + 1;
-  const int p0 = chunk * SPC * C;
-  const bool active = p0 < L;
   const bool owner = pos >= p0 && pos < p0 + SPC * C;
   const half_t* kh = kc + (size_t)h * max_seq * D;
   const half_t* vh = vc + (size_t)h * max_seq * D;
-  const int dg = lane & 15, pq = (lane >> 4) + 4 * wave;   // P.V: elements 8dg.., positions 4pq..4pq+3
+  const int dg = lane & 15, q4 = lane >> 4;   // V rows: elements 8dg.., the wave's positions 4q4 .. 4q4+3
 
+  // 1) The prologue's operands: query heads wave and wave + 4, the new
+  //    key (owner wave 0) or value (owner wave 1), norm weights, cos / sin.
+  const half2_t c2 = reinterpret_cast<const half2_t*>(cos_t + (size_t)pos * D)[lane];
+  const half2_t s2 = reinterpret_cast<const half2_t*>(sin_t + (size_t)pos * D)[lane];
+  half2_t qv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int g = wave + 4 * j;
+    qv[j] = g < G ? reinterpret_cast<const half2_t*>(qkv + (size_t)(h * G + g) * D)[lane] : half2_t{};
+  }
+  const half2_t nq = qn_w ? reinterpret_cast<const half2_t*>(qn_w)[lane] : half2_t{};
+  half2_t nv = {}, nk = {};
+  if (owner && wave == 0) {
+    nv = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + h) * D)[lane];
+    if (kn_w) nk = reinterpret_cast<const half2_t*>(kn_w)[lane];
+  }
+  if (owner && wave == 1) nv = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + KV + h) * D)[lane];
+
+  // 2) The cache stream.
   uint4_t kr[SPC][4], vr[SPC][4];
-  if (active) {
 #pragma unroll
-    for (int s = 0; s < SPC; ++s) {
-      const int rk = min(p0 + s * C + 16 * wave + i, max_seq - 1);
-      const uint4_t* ks_src = reinterpret_cast<const uint4_t*>(kh + (size_t)rk * D + 8 * kb);
+  for (int s = 0; s < SPC; ++s) {
+    const int pw0 = p0 + s * C + 16 * wave;
+    const int rk = min(pw0 + i, max_seq - 1);
+    const uint4_t* ks_src = reinterpret_cast<const uint4_t*>(kh + (size_t)rk * D + 8 * kb);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kr[s][ks] = ks_src[4 * ks];
+    for (int ks = 0; ks < 4; ++ks) kr[s][ks] = ks_src[4 * ks];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rv = min(pw0 + 4 * q4 + e, max_seq - 1);
+      vr[s][e] = *reinterpret_cast<const uint4_t*>(vh + (size_t)rv * D + 8 * dg);
+    }
+  }
+
+  // 3) q / k RMSNorm + RoPE, the cache append.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int g = wave + 4 * j;
+    const half2_t r = g < G ? norm_rope_pair(qv[j], qn_w != nullptr, nq, eps, c2, s2, lane) : half2_t{};
+    reinterpret_cast<half2_t*>(qh[g])[lane] = r;
+  }
+  if (owner && wave == 0) {
+    const half2_t r = norm_rope_pair(nv, kn_w != nullptr, nk, eps, c2, s2, lane);
+    reinterpret_cast<half2_t*>(knew)[lane] = r;
+    reinterpret_cast<half2_t*>(kc + (size_t)h * max_seq * D + (size_t)pos * D)[lane] = r;
+  }
+  if (owner && wave == 1) {
+    reinterpret_cast<half2_t*>(vnew)[lane] = nv;
+    reinterpret_cast<half2_t*>(vc + (size_t)h * max_seq * D + (size_t)pos * D)[lane] = nv;
+  }
+  __syncthreads();
+
+  half8_t qa[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    qa[ks] = i < GM ? *reinterpret_cast<const half8_t*>(&qh[i < GM ? i : 0][32 * ks + 8 * kb]) : half8_t{};
+  float4_t oacc[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) oacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[4], l_run[4];   // heads 4kb + v, the same in all 16 lanes of the row
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    m_run[v] = -INFINITY;
+    l_run[v] = 0.f;
+  }
+
+#pragma unroll
+  for (int s = 0; s < SPC; ++s) {
+    const int ps = p0 + s * C + 16 * wave;   // the wave's first position (wave-uniform)
+    if (ps < L) {
+      const int pk = ps + i;
+      if (pk == pos) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kr[s][ks] = *reinterpret_cast<const uint4_t*>(knew + 32 * ks + 8 * kb);
+      }
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc = mfma16(qa[ks], __builtin_bit_cast(half8_t, kr[s][ks]), acc);
+      // Position ps < L is in every row, so each row max is finite.
+      float pv[4], alpha[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float sv = pk < L ? acc[v] * scale_log2 : -INFINITY;
+        const float mn = fmaxf(m_run[v], row_max16(sv));
+        pv[v] = exp2_hw(sv - mn);           // -inf -> 0
+        alpha[v] = exp2_hw(m_run[v] - mn);  // 0 on the wave's first sub-chunk
+        l_run[v] = l_run[v] * alpha[v] + row_sum16(pv[v]);
+        m_run[v] = mn;
+      }
+      // Rows past L carry P = 0 and are zeroed (0 * NaN would poison the
+      // sum); row `pos` comes from LDS.
+      half8_t v8[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int rv = min(p0 + s * C + 4 * pq + e, max_seq - 1);
-        vr[s][e] = *reinterpret_cast<const uint4_t*>(vh + (size_t)rv * D + 8 * dg);
+        const int p = ps + 4 * q4 + e;
+        v8[e] = p == pos ? *reinterpret_cast<const half8_t*>(vnew + 8 * dg)
+                         : (p < L ? __builtin_bit_cast(half8_t, vr[s][e]) : half8_t{});
+      }
+      wave_lds_sync();   // the previous sub-chunk's fragment reads are done
+#pragma unroll
+      for (int v = 0; v < 4; ++v) pl[wave][4 * kb + v][i] = (half_t)pv[v];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        *reinterpret_cast<half4_t*>(&vt[wave][8 * dg + k][4 * q4]) = half4_t{v8[0][k], v8[1][k], v8[2][k], v8[3][k]};
+      wave_lds_sync();
+      const half4_t pa = *reinterpret_cast<const half4_t*>(&pl[wave][i][4 * kb]);
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t) {
+        const half4_t vb = *reinterpret_cast<const half4_t*>(&vt[wave][16 * t + i][4 * kb]);
+        float4_t o = oacc[t];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] *= alpha[v];
+        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, o, 0, 0, 0);
       }
     }
   }
 
-  if (active) {
-    const half_t* cs = cos_t + (size_t)pos * D;
-    const half_t* sn = sin_t + (size_t)pos * D;
-    for (int g = wave; g < GM; g += 4) {
-      half2_t r = {};
-      if (g < G) {
-        const half2_t v = reinterpret_cast<const half2_t*>(qkv + (size_t)(h * G + g) * D)[lane];
-        r = norm_rope_pair(v, qn_w, eps, cs, sn, lane);
+  // oacc[t][v] = this wave's unnormalized output of head 4kb + v at
+  // d = 16t + i (a wave with no position below L holds zeros, max -inf).
+  if (kb < 2) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (4 * kb + v < G) {
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) red[wave][4 * kb + v][16 * t + i] = oacc[t][v];
       }
-      reinterpret_cast<half2_t*>(qh[g])[lane] = r;
-    }
-    if (owner && wave == 0) {
-      const half2_t v = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + h) * D)[lane];
-      const half2_t r = norm_rope_pair(v, kn_w, eps, cs, sn, lane);
-      reinterpret_cast<half2_t*>(knew)[lane] = r;
-      reinterpret_cast<half2_t*>(kc + (size_t)h * max_seq * D + (size_t)pos * D)[lane] = r;
-    }
-    if (owner && wave == 1) {
-      const half2_t v = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + KV + h) * D)[lane];
-      reinterpret_cast<half2_t*>(vnew)[lane] = v;
-      reinterpret_cast<half2_t*>(vc + (size_t)h * max_seq * D + (size_t)pos * D)[lane] = v;
-    }
   }
-  __syncthreads();
-
-  float o[G][8];
+  if (i == 0 && kb < 2) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int k = 0; k < 8; ++k) o[g][k] = 0.f;
-  const int srow = lane >> 4, sj = lane & 15, sg = 4 * wave + srow;
-  float m_run = -INFINITY, l_run = 0.f;
-
-  if (active) {
-    half8_t qa[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qa[ks] = i < GM ? *reinterpret_cast<const half8_t*>(&qh[i < GM ? i : 0][32 * ks + 8 * kb]) : half8_t{};
-#pragma unroll
-    for (int s = 0; s < SPC; ++s) {
-      const int ps = p0 + s * C;
-      if (ps < L) {
-        const int pk = ps + 16 * wave + i;
-        if (pk == pos) {
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) kr[s][ks] = *reinterpret_cast<const uint4_t*>(knew + 32 * ks + 8 * kb);
-        }
-        float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = mfma16(qa[ks], __builtin_bit_cast(half8_t, kr[s][ks]), acc);
-        if (kb < 2) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) sc[4 * kb + v][16 * wave + i] = pk < L ? acc[v] * scale : -INFINITY;
-        }
-        __syncthreads();
-        if (sg < G) {
-          float4_t x = *reinterpret_cast<const float4_t*>(&sc[sg][4 * sj]);
-          const float m_new = fmaxf(m_run, row_max16(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))));   // finite
-          float es = 0.f;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            x[e] = x[e] == -INFINITY ? 0.f : expf(x[e] - m_new);
-            es += x[e];
-          }
-          const float a = expf(m_run - m_new);   // 0 on the first sub-chunk
-          l_run = l_run * a + row_sum16(es);
-          m_run = m_new;
-          *reinterpret_cast<float4_t*>(&sc[sg][4 * sj]) = x;
-          if (sj == 0) alph[sg] = a;
-        }
-        __syncthreads();
-        // Rows past L carry P = 0; row `pos` comes from LDS, clamped or stale
-        // rows are zeroed so that 0 * garbage cannot produce NaN.
-        half8_t v8[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int p = ps + 4 * pq + e;
-          v8[e] = p == pos ? *reinterpret_cast<const half8_t*>(vnew + 8 * dg)
-                           : (p < L ? __builtin_bit_cast(half8_t, vr[s][e]) : half8_t{});
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float a = alph[g];
-          const float4_t pr = *reinterpret_cast<const float4_t*>(&sc[g][4 * pq]);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            float t = o[g][k] * a;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) t += pr[e] * (float)v8[e][k];
-            o[g][k] = t;
-          }
-        }
-        __syncthreads();
-      }
-    }
-    if (sg < G && sj == 0) {
-      mls[sg][0] = m_run;
-      mls[sg][1] = l_run;
-    }
-    // Sum the four position quads of this wave (lanes dg, dg+16, dg+32, dg+48).
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        float t = o[g][k];
-        t += __shfl_xor(t, 16);
-        t += __shfl_xor(t, 32);
-        o[g][k] = t;
-      }
-    if (lane < 16) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float* dst = red + (wave * GM + g) * D + 8 * dg;
-        *reinterpret_cast<float4_t*>(dst) = float4_t{o[g][0], o[g][1], o[g][2], o[g][3]};
-        *reinterpret_cast<float4_t*>(dst + 4) = float4_t{o[g][4], o[g][5], o[g][6], o[g][7]};
-      }
+    for (int v = 0; v < 4; ++v) {
+      mlw[wave][4 * kb + v][0] = m_run[v];
+      mlw[wave][4 * kb + v][1] = l_run[v];
     }
   }
   __syncthreads();
 
-  if (NC == 1) {
-    for (int j = tid; j < G * D; j += 256) {
-      const int g = j / D, d = j % D;
-      const float o = red[g * D + d] + red[(GM + g) * D + d] + red[(2 * GM + g) * D + d] + red[(3 * GM + g) * D + d];
-      out[(size_t)(h * G + g) * D + d] = (half_t)(o / mls[g][1]);
-    }
-    return;
-  }
-  // Several chunks: publish this chunk's partial for decode_attention_merge
-  // (the next launch on the stream).
-  if (active) {
-    if (tid < G * (D / 4)) {
-      const int g = tid / (D / 4), d = 4 * (tid % (D / 4));
-      float4_t o;
+  // Combine the four waves (a wave with no position below L has max -inf,
+  // sum 0 and output 0; wave 0 always has one, so M is finite).
+  for (int j = tid; j < G * (D / 4); j += 256) {
+    const int g = j / (D / 4), d = 4 * (j % (D / 4));
+    float M = mlw[0][g][0];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = red[g * D + d + e] + red[(GM + g) * D + d + e] + red[(2 * GM + g) * D + d + e] +
-               red[(3 * GM + g) * D + d + e];
-      *reinterpret_cast<float4_t*>(ws_o + (((size_t)(h * NC + chunk) * G + g) * D + d)) = o;
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, mlw[w][g][0]);
+    float4_t num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float wt = exp2_hw(mlw[w][g][0] - M);
+      num += wt * *reinterpret_cast<const float4_t*>(&red[w][g][d]);
+      den += wt * mlw[w][g][1];
     }
-    if (tid < 2 * G) ws_ml[((size_t)(h * NC + chunk) * G) * 2 + tid] = mls[tid >> 1][tid & 1];
+    if (NC == 1) {
+      half4_t r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = (half_t)(num[e] / den);
+      *reinterpret_cast<half4_t*>(out + (size_t)(h * G + g) * D + d) = r;
+    } else {
+      const size_t slot = (size_t)(h * G + g) * NC + chunk;
+      *reinterpret_cast<float4_t*>(ws_o + slot * D + d) = num;
+      if (d == 0) {
+        ws_ml[slot * 2] = M;
+        ws_ml[slot * 2 + 1] = den;
+      }
+    }
   }
 }
 
 // Merge of the chunk partials of one query head: grid = q_heads, 128 threads
-// (one output element each).  All of the head's partial outputs are
-// requested before the maxima are known, then combined in chunk order:
-// out = sum_c exp(m_c - M) O_c / sum_c exp(m_c - M) l_c.
-__global__ __launch_bounds__(128) void decode_attention_merge_kernel(const int32_t* __restrict__ position, int G,
-                                                                     int NC, int chunk_positions, int max_seq,
-                                                                     const float* __restrict__ ws_o,
-                                                                     const float* __restrict__ ws_ml,
+// (one output element each).  The partial outputs are requested at once (at
+// chunk indices clamped below NC); meanwhile wave 0 turns the chunks' (max,
+// sum) pairs, one per lane, into weights w_c = 2^(m_c - M) (0 for an empty
+// chunk, whose output slot holds zeros) and their weighted sum.  Then
+// out = sum_c w_c O_c / sum_c w_c l_c, summed in chunk order.  With no
+// non-empty chunk (invalid position) the result is 0 / 0 = NaN.
+__global__ __launch_bounds__(128) void decode_attention_merge_kernel(int NC, const float* __restrict__ ws_o,
+                                                                     const float2_t* __restrict__ ws_ml,
                                                                      half_t* __restrict__ out) {
   constexpr int D = kHeadDim;
-  __shared__ float ms[kMaxChunks], ls[kMaxChunks];
-  const int qh = blockIdx.x, h = qh / G, g = qh % G, d = threadIdx.x;
-  const int pos = *position;
-  if (pos < 0 || pos >= max_seq) return;   // the attention launch already wrote NaN
-  const int NA = min((pos + chunk_positions) / chunk_positions, NC);   // chunks holding positions 0..pos
+  __shared__ __attribute__((aligned(16))) float sw[kMaxChunks];
+  __shared__ float sden;
+  const int qh = blockIdx.x, d = threadIdx.x;
+  const float* po = ws_o + (size_t)qh * NC * D + d;
   float part[kMaxChunks];
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c)
-    part[c] = c < NA ? ws_o[((size_t)(h * NC + c) * G + g) * D + d] : 0.f;
-  if (d < NA) {
-    ms[d] = ws_ml[((size_t)(h * NC + d) * G + g) * 2];
-    ls[d] = ws_ml[((size_t)(h * NC + d) * G + g) * 2 + 1];
+  for (int c = 0; c < kMaxChunks; ++c) part[c] = po[(size_t)min(c, NC - 1) * D];
+  if (d < 64) {
+    const float2_t ml = d < NC ? ws_ml[(size_t)qh * NC + d] : float2_t{-INFINITY, 0.f};
+    const float M = wave_max(ml.x);
+    const float w = ml.x == -INFINITY ? 0.f : exp2_hw(ml.x - M);
+    sw[d] = w;
+    const float den = wave_sum(w * ml.y);
+    if (d == 0) sden = den;
   }
   __syncthreads();
-  float M = -INFINITY;
-  for (int c = 0; c < NA; ++c) M = fmaxf(M, ms[c]);
-  float num = 0.f, den = 0.f;
+  float num = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c)
-    if (c < NA) {
-      const float w = expf(ms[c] - M);
-      num += w * part[c];
-      den += w * ls[c];
-    }
-  out[(size_t)qh * D + d] = (half_t)(num / den);
+  for (int c = 0; c < kMaxChunks; ++c) num += sw[c] * part[c];
+  out[(size_t)qh * D + d] = (half_t)(num / sden);
 }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -479,7 +510,7 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
   const int64_t nc = split.nc;
   const size_t need = attention_workspace_bytes(q_heads, kv_heads, max_seq);
   WQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), WQ_ERR_WORKSPACE,
-             "decode attention needs a zero-filled workspace of %zu bytes (got %zu)", need, workspace_bytes);
+             "decode attention needs a workspace of %zu bytes (got %zu)", need, workspace_bytes);
   float* ml = need ? reinterpret_cast<float*>(workspace) : nullptr;
   float* po = need ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) +
                                               align256((size_t)kv_heads * nc * (q_heads / kv_heads) * 2 * 4))
@@ -490,7 +521,7 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
                        reinterpret_cast<const half_t*>(q_norm_weight), reinterpret_cast<const half_t*>(k_norm_weight),
                        eps, reinterpret_cast<const half_t*>(cos_table), reinterpret_cast<const half_t*>(sin_table),
                        position, reinterpret_cast<half_t*>(key_cache), reinterpret_cast<half_t*>(value_cache),
-                       (int)max_seq, scale, reinterpret_cast<half_t*>(out), po, ml);
+                       (int)max_seq, scale * kLog2e, reinterpret_cast<half_t*>(out), po, ml);
   };
   const int g = (int)(q_heads / kv_heads);
 #define WQ_ATTN_CASE(GG)                                                                     \
@@ -507,7 +538,7 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
     const int rc2 = check_launch("decode_attention");
     if (rc2 != WQ_OK) return rc2;
     hipLaunchKernelGGL(decode_attention_merge_kernel, dim3((unsigned)q_heads), dim3(kHeadDim), 0, as_stream(stream),
-                       position, g, (int)nc, split.spc * kSub, (int)max_seq, po, ml, reinterpret_cast<half_t*>(out));
+                       (int)nc, po, reinterpret_cast<const float2_t*>(ml), reinterpret_cast<half_t*>(out));
     return check_launch("decode_attention_merge");
   }
   return check_launch("decode_attention");

@@ -326,14 +326,13 @@ __device__ __forceinline__ uint4_t rms_scale8(uint4_t xv, uint4_t wv, float r) {
 }
 
 // Eight (gate, up) pairs -> fp16(fp16(silu(gate)) * up), as F.silu on an
-// fp16 tensor followed by an fp16 product.
+// fp16 tensor followed by an fp16 product (silu in fp32, see silu_f).
 __device__ __forceinline__ uint4_t silu_mul8(uint4_t gv, uint4_t uv) {
   const half8_t gh = __builtin_bit_cast(half8_t, gv), uh = __builtin_bit_cast(half8_t, uv);
   half8_t o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float g = (float)gh[e];
-    o[e] = (half_t)(g / (1.0f + expf(-g))) * uh[e];
+    o[e] = (half_t)silu_f((float)gh[e]) * uh[e];
   }
   return __builtin_bit_cast(uint4_t, o);
 }
@@ -391,6 +390,16 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
 #pragma unroll
     for (int u = 0; u < kSqPerLane; ++u) sq[u] = fz.sumsq_in[min(lane + 64 * u, fz.sumsq_count - 1)];
   }
+  // The fused residual (W4, M = 1; wave 0 stores the tile) is fetched now so
+  // that its latency is not added after the reduction (for NB <= 8, where the
+  // two registers are free).  Every split reads it before it counts in, so
+  // an aliased y still holds the old value here.
+  constexpr bool kEarlyResidual = F == WFmt::W4 && NB <= 8;
+  const bool has_x = i < M;
+  const int n0 = tile * 16 + 4 * kb;
+  half4_t res = {};
+  if (kEarlyResidual && fz.residual && wave == 0 && has_x && n0 < N)
+    res = *reinterpret_cast<const half4_t*>(fz.residual + n0);
   int g_lo = 0;
   uint2_t mr[kMPerLane > 0 ? kMPerLane : 1];
   if constexpr (F == WFmt::W4) {
@@ -450,7 +459,6 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
     for (int j = 0; j < kMPerLane; ++j) reinterpret_cast<uint2_t*>(ml)[lane + 64 * j] = mr[j];
   }
 
-  const bool has_x = i < M;
   half8_t xv[4] = {half8_t{}, half8_t{}, half8_t{}, half8_t{}};   // columns m >= M stay zero
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
   auto consume = [&](const BlockRegs<F>& wb, int s2) {
@@ -525,7 +533,6 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
     if (lane == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (has_x) {
-    const int n0 = tile * 16 + 4 * kb;
     if constexpr (F == WFmt::W4) {
       half4_t o;
 #pragma unroll
@@ -533,7 +540,7 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
       if (n0 < N) {
         // Fused residual (M = 1): y = residual + fp16(x.W^T), as the
         // reference adds the rounded projection to the fp16 residual.
-        if (fz.residual) o = *reinterpret_cast<const half4_t*>(fz.residual + n0) + o;
+        if (fz.residual) o = (kEarlyResidual ? res : *reinterpret_cast<const half4_t*>(fz.residual + n0)) + o;
         *reinterpret_cast<half4_t*>(y + (size_t)i * N + n0) = o;
       }
       if (fz.sumsq_out) {

@@ -110,8 +110,9 @@ def _run(nat, case, t, qkv, pos, ws):
 ])
 def test_decode_attention_matches_oracle(nat, h, kv, max_seq, positions):
     case = AttnCase(h, kv, max_seq, seed=h + max_seq)
-    ws = torch.zeros(max(nat.decode_attention_workspace_size(h, kv, 128, max_seq), 1), dtype=torch.uint8,
-                     device='cuda')
+    # All-ones bytes (NaN floats): the workspace needs no initialization.
+    ws = torch.full((max(nat.decode_attention_workspace_size(h, kv, 128, max_seq), 1),), 255, dtype=torch.uint8,
+                    device='cuda')
     for pos in positions:
         print(f'[decode_attention] h={h} kv={kv} max_seq={max_seq} pos={pos}', flush=True)
         case.kc[:] = np.nan
