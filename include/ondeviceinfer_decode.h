@@ -52,7 +52,7 @@ int wq_decode_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_
  * Replaces: q/k rms_norm + apply_rotary_pos_emb + ResidentKVCache.update +
  * F.scaled_dot_product_attention(enable_gqa=True) for query_length 1
  * (quantized_model.py:171-199, layers.py:64-80, cache.py:60-80,
- * attention.py:35-85).  max_seq <= 8192, q_heads / kv_heads <= 8.  A
+ * attention.py:35-85).  max_seq <= 16384, q_heads / kv_heads <= 8.  A
  * position outside [0, max_seq) writes NaN to out and leaves the cache
  * untouched. */
 int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t kv_heads, int64_t head_dim,

@@ -30,7 +30,7 @@ WQ_ERR_WORKSPACE = 4
 ABI_VERSION = 1
 
 W4_BLOCK_K = 128
-DECODE_ATTENTION_MAX_SEQ = 8192   # wq_decode_attention: 64 workgroups x 2 sub-chunks x 64 positions per kv head
+DECODE_ATTENTION_MAX_SEQ = 16384   # wq_decode_attention: 64 workgroups x 4 sub-chunks x 64 positions per kv head
 W4_META_BYTES = 40
 W8_BLOCK_K = 128
 

@@ -18,10 +18,11 @@ namespace wq {
 namespace {
 
 constexpr int kHeadDim = 128;     // Qwen3 head_dim; one lane holds two elements
-constexpr int kSub = 64;          // KV positions per attention sub-chunk (one per lane of a softmax wave)
+constexpr int kBlock = 16;        // KV positions per attention block (one wave's matrix tile)
 constexpr int kMaxGroup = 8;      // q heads per kv head
-constexpr int kMaxChunks = 64;    // attention workgroups per kv head
-constexpr int kMaxSpc = 2;        // sub-chunks per workgroup
+constexpr int kSub = 4 * kBlock;  // KV positions per attention sub-chunk (one block per wave)
+constexpr int kMaxChunks = 64;    // attention workgroups per kv head (one merge thread each)
+constexpr int kMaxSpc = 4;        // sub-chunks per workgroup
 constexpr int kMaxSeq = kMaxChunks * kMaxSpc * kSub;
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -136,17 +137,22 @@ __device__ __forceinline__ half2_t norm_rope_pair(half2_t v, bool norm, half2_t 
   return t1 + t2;
 }
 
-// Split of a kv head's positions over workgroups: `spc` (1 or 2) sub-chunks
-// of 64 positions per workgroup, so that no head has more than kMaxChunks
-// workgroups (the merge reads one partial per workgroup).
+// Work split of the attention: a kv head's positions go to `nc` workgroups
+// of `spc` (1 .. 4) consecutive sub-chunks of 64 positions, spc the fewest
+// that keep nc <= kMaxChunks (the merge reads one partial per workgroup).
+// Within a sub-chunk wave w takes the block of positions 16w .. 16w + 15.
+// Measured against other splits of the same cache on MI355X (fixed grids of
+// 256 - 1024 workgroups with blocks dealt round-robin, or fewer, longer
+// chunks), this one, about one workgroup per compute unit at 4K positions
+// and 8 kv heads, streams fastest and keeps the merge short.
 struct AttnSplit {
   int spc, nc;
 };
 
 AttnSplit attn_split(int64_t max_seq) {
   const int64_t subs = (max_seq + kSub - 1) / kSub;
-  const int spc = (int)((subs + kMaxChunks - 1) / kMaxChunks);
-  return {spc, (int)((subs + spc - 1) / spc)};
+  const int64_t spc = (subs + kMaxChunks - 1) / kMaxChunks;
+  return {(int)spc, (int)((subs + spc - 1) / spc)};
 }
 
 // Orders this wave's LDS accesses around a wave-private exchange (the
@@ -159,18 +165,18 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// grid = (kv_heads, chunks); 256 threads = 4 waves.  Workgroup c of kv head
-// h covers positions [c * SPC * 64, (c + 1) * SPC * 64); in each sub-chunk of
-// 64 positions wave w owns positions 16w .. 16w + 15 and runs its own online
-// softmax over them for the head's G <= 8 query heads, so the sub-chunk loop
-// has no workgroup barrier.  Lane l is (r, i) = (l / 16, l % 16).
+// grid = (kv_heads, nc); 256 threads = 4 waves.  Workgroup c of kv head h
+// covers positions [c * SPC * 64, (c + 1) * SPC * 64); in each sub-chunk
+// wave w owns the block 16w .. 16w + 15 and runs its own online softmax over
+// its blocks for the head's G <= 8 query heads, so the block loop has no
+// workgroup barrier.  Lane l is (r, i) = (l / 16, l % 16).
 //   loads   the prologue's operands (q, cos/sin rows, norm weights, the new
-//           k/v) are requested first, then every K fragment and V row this
-//           workgroup needs (rows clamped into the cache; rows past L or at
+//           k/v) are requested first, then every K fragment and V row of the
+//           wave's blocks (rows clamped into the cache; rows past L or at
 //           `pos` are replaced below), so the q/k prologue runs while the
 //           cache streams in;
 //   scores  S[g][p] = q_g . k_p on the matrix cores (16x16x32): A = the query
-//           heads (rows g, zero past G), B = the wave's 16 key rows (each
+//           heads (rows g, zero past G), B = the block's 16 key rows (each
 //           lane 16 bytes of one row); lane (r, i) gets heads 4r .. 4r+3 at
 //           position i, in log2 units (scale * log2 e);
 //   softmax the 16 lanes of DPP row r reduce max and sum for heads 4r + v;
@@ -180,21 +186,21 @@ __device__ __forceinline__ void wave_lds_sync() {
 //           MFMA per 16 values of d; the accumulator rows are the heads 4r+v
 //           of the lane's own softmax row, so the online rescale is local.
 // At the end the four waves' (max, sum, output) are combined through LDS.
-// The workgroup whose chunk holds `pos` also normalizes, rotates and appends
-// the new key and value and takes them from LDS.  With one chunk per head
-// the workgroup writes the output; otherwise every chunk, active or not,
-// writes its (max, sum) pair and unnormalized output to the workspace, and
-// decode_attention_merge_kernel (the next launch) combines them without
-// reading the position: an empty chunk writes (-inf, 0) and zeros and weighs
-// nothing, and an invalid position leaves every max at -inf, which the merge
-// turns into NaN.
+// The workgroup that holds `pos` also normalizes, rotates and appends the
+// new key and value, and takes them from LDS.  With one
+// workgroup per head it writes the output; otherwise every workgroup, active
+// or not, writes its (max, sum) pair and unnormalized output to the
+// workspace, and decode_attention_merge_kernel (the next launch) combines
+// them without reading the position: an empty workgroup writes (-inf, 0) and
+// zeros and weighs nothing, and an invalid position leaves every max at
+// -inf, which the merge turns into NaN.
 template <int G, int SPC>
 __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
     const half_t* __restrict__ qkv, int H, int KV, const half_t* __restrict__ qn_w,
     const half_t* __restrict__ kn_w, float eps, const half_t* __restrict__ cos_t, const half_t* __restrict__ sin_t,
     const int32_t* __restrict__ position, half_t* kc, half_t* vc, int max_seq, float scale_log2,
     half_t* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  constexpr int D = kHeadDim, C = kSub, GM = kMaxGroup;
+  constexpr int D = kHeadDim, GM = kMaxGroup;
   constexpr int VTS = 20;   // V^T row stride in halves (40 bytes: the 16 B-fragment reads hit distinct banks)
   __shared__ __attribute__((aligned(16))) half_t qh[GM][D];
   __shared__ __attribute__((aligned(16))) half_t knew[D];
@@ -210,9 +216,9 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   const int pos = *position;
   const bool valid = pos >= 0 && pos < max_seq;
   const int L = valid ? pos + 1 : 0;
-  const int p0 = chunk * SPC * C;
+  const int p0 = chunk * SPC * kSub;
   if (p0 >= L) {
-    // Nothing to attend in this chunk (every chunk, when the position is
+    // Nothing to attend in this chunk (in any chunk when the position is
     // invalid; chunk 0 is active whenever it is valid).
     if (NC == 1) {
       for (int j = tid; j < G * D; j += 256) out[(size_t)h * G * D + j] = (half_t)__builtin_nanf("");
@@ -228,10 +234,10 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
     }
     return;
   }
-  const bool owner = pos >= p0 && pos < p0 + SPC * C;
+  const bool owner = pos >= p0 && pos < p0 + SPC * kSub;
   const half_t* kh = kc + (size_t)h * max_seq * D;
   const half_t* vh = vc + (size_t)h * max_seq * D;
-  const int dg = lane & 15, q4 = lane >> 4;   // V rows: elements 8dg.., the wave's positions 4q4 .. 4q4+3
+  const int dg = lane & 15, q4 = lane >> 4;   // V rows: elements 8dg.., the block's positions 4q4 .. 4q4+3
 
   // 1) The prologue's operands: query heads wave and wave + 4, the new
   //    key (owner wave 0) or value (owner wave 1), norm weights, cos / sin.
@@ -251,23 +257,25 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   }
   if (owner && wave == 1) nv = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + KV + h) * D)[lane];
 
-  // 2) The cache stream.
+  // 2) The cache stream: this wave's block of sub-chunk j starts at pb.
   uint4_t kr[SPC][4], vr[SPC][4];
 #pragma unroll
-  for (int s = 0; s < SPC; ++s) {
-    const int pw0 = p0 + s * C + 16 * wave;
-    const int rk = min(pw0 + i, max_seq - 1);
+  for (int j = 0; j < SPC; ++j) {
+    const int pb = p0 + j * kSub + kBlock * wave;
+    const int rk = min(pb + i, max_seq - 1);
     const uint4_t* ks_src = reinterpret_cast<const uint4_t*>(kh + (size_t)rk * D + 8 * kb);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kr[s][ks] = ks_src[4 * ks];
+    for (int ks = 0; ks < 4; ++ks) kr[j][ks] = ks_src[4 * ks];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int rv = min(pw0 + 4 * q4 + e, max_seq - 1);
-      vr[s][e] = *reinterpret_cast<const uint4_t*>(vh + (size_t)rv * D + 8 * dg);
+      const int rv = min(pb + 4 * q4 + e, max_seq - 1);
+      vr[j][e] = *reinterpret_cast<const uint4_t*>(vh + (size_t)rv * D + 8 * dg);
     }
   }
 
-  // 3) q / k RMSNorm + RoPE, the cache append.
+  // 3) q / k RMSNorm + RoPE; the new key and value go to LDS and are
+  //    appended to the cache (this workgroup's loads of row `pos` were
+  //    issued before and are replaced by the LDS copies).
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int g = wave + 4 * j;
@@ -301,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
 
 #pragma unroll
   for (int s = 0; s < SPC; ++s) {
-    const int ps = p0 + s * C + 16 * wave;   // the wave's first position (wave-uniform)
+    const int ps = p0 + s * kSub + kBlock * wave;   // the block's first position (wave-uniform)
     if (ps < L) {
       const int pk = ps + i;
       if (pk == pos) {
@@ -351,7 +359,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   }
 
   // oacc[t][v] = this wave's unnormalized output of head 4kb + v at
-  // d = 16t + i (a wave with no position below L holds zeros, max -inf).
+  // d = 16t + i (a wave with no block holds zeros, max -inf).
   if (kb < 2) {
 #pragma unroll
     for (int v = 0; v < 4; ++v)
@@ -400,36 +408,39 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   }
 }
 
-// Merge of the chunk partials of one query head: grid = q_heads, 128 threads
-// (one output element each).  The partial outputs are requested at once (at
-// chunk indices clamped below NC); meanwhile wave 0 turns the chunks' (max,
-// sum) pairs, one per lane, into weights w_c = 2^(m_c - M) (0 for an empty
-// chunk, whose output slot holds zeros) and their weighted sum.  Then
-// out = sum_c w_c O_c / sum_c w_c l_c, summed in chunk order.  With no
-// non-empty chunk (invalid position) the result is 0 / 0 = NaN.
+// Merge of the workgroup partials of one query head: grid = q_heads, 128
+// threads (one output element each).  The NC <= NCM partial outputs are
+// requested at once (at chunk indices clamped below NC); meanwhile wave 0
+// turns the chunks' (max, sum) pairs, one per lane, into weights
+// w_c = 2^(m_c - M) (0 for an empty chunk, whose output slot holds zeros)
+// and their weighted sum.  Then out = sum_c w_c O_c / sum_c w_c l_c, summed
+// in chunk order.  With no non-empty chunk (invalid position) the result is
+// 0 / 0 = NaN.
+template <int NCM>
 __global__ __launch_bounds__(128) void decode_attention_merge_kernel(int NC, const float* __restrict__ ws_o,
                                                                      const float2_t* __restrict__ ws_ml,
                                                                      half_t* __restrict__ out) {
   constexpr int D = kHeadDim;
+  static_assert(NCM <= kMaxChunks && kMaxChunks <= 64, "wave 0 holds one chunk per lane");
   __shared__ __attribute__((aligned(16))) float sw[kMaxChunks];
   __shared__ float sden;
   const int qh = blockIdx.x, d = threadIdx.x;
   const float* po = ws_o + (size_t)qh * NC * D + d;
-  float part[kMaxChunks];
+  float part[NCM];
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) part[c] = po[(size_t)min(c, NC - 1) * D];
+  for (int c = 0; c < NCM; ++c) part[c] = po[(size_t)min(c, NC - 1) * D];
   if (d < 64) {
     const float2_t ml = d < NC ? ws_ml[(size_t)qh * NC + d] : float2_t{-INFINITY, 0.f};
     const float M = wave_max(ml.x);
     const float w = ml.x == -INFINITY ? 0.f : exp2_hw(ml.x - M);
-    sw[d] = w;
+    if (d < kMaxChunks) sw[d] = w;
     const float den = wave_sum(w * ml.y);
     if (d == 0) sden = den;
   }
   __syncthreads();
   float num = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) num += sw[c] * part[c];
+  for (int c = 0; c < NCM; ++c) num += sw[c] * part[c];
   out[(size_t)qh * D + d] = (half_t)(num / sden);
 }
 
@@ -526,7 +537,12 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
   const int g = (int)(q_heads / kv_heads);
 #define WQ_ATTN_CASE(GG)                                                                     \
   case GG:                                                                                   \
-    if (split.spc == 1) launch(decode_attention_kernel<GG, 1>); else launch(decode_attention_kernel<GG, 2>); \
+    switch (split.spc) {                                                                     \
+      case 1: launch(decode_attention_kernel<GG, 1>); break;                                 \
+      case 2: launch(decode_attention_kernel<GG, 2>); break;                                 \
+      case 3: launch(decode_attention_kernel<GG, 3>); break;                                 \
+      default: launch(decode_attention_kernel<GG, 4>); break;                                \
+    }                                                                                        \
     break;
   switch (g) {
     WQ_ATTN_CASE(1) WQ_ATTN_CASE(2) WQ_ATTN_CASE(3) WQ_ATTN_CASE(4)
@@ -537,8 +553,9 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
   if (nc > 1) {
     const int rc2 = check_launch("decode_attention");
     if (rc2 != WQ_OK) return rc2;
-    hipLaunchKernelGGL(decode_attention_merge_kernel, dim3((unsigned)q_heads), dim3(kHeadDim), 0, as_stream(stream),
-                       (int)nc, po, reinterpret_cast<const float2_t*>(ml), reinterpret_cast<half_t*>(out));
+    auto merge = nc <= 32 ? decode_attention_merge_kernel<32> : decode_attention_merge_kernel<64>;
+    hipLaunchKernelGGL(merge, dim3((unsigned)q_heads), dim3(kHeadDim), 0, as_stream(stream), (int)nc, po,
+                       reinterpret_cast<const float2_t*>(ml), reinterpret_cast<half_t*>(out));
     return check_launch("decode_attention_merge");
   }
   return check_launch("decode_attention");

@@ -103,7 +103,9 @@ def _run(nat, case, t, qkv, pos, ws):
 
 
 @pytest.mark.parametrize('h,kv,max_seq,positions', [
-    (40, 8, 4224, (0, 1, 63, 64, 65, 1000, 4223)),   # Qwen3-14B geometry at a 4K+128 cache
+    (40, 8, 4224, (0, 1, 15, 16, 63, 64, 65, 1000, 4095, 4096, 4223)),   # Qwen3-14B at a 4K+128 cache
+    (40, 8, 16384, (0, 255, 256, 9000, 16383)),      # largest cache: 64 workgroups of 4 sub-chunks
+    (8, 4, 9000, (0, 191, 192, 8999)),                # 47 workgroups of 3 sub-chunks
     (40, 8, 64, (0, 10, 63)),                         # one chunk: no cross-workgroup merge
     (64, 8, 300, (0, 129, 299)),                      # 8 query heads per kv head
     (8, 8, 200, (5, 199)),                            # no grouping

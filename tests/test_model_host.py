@@ -132,13 +132,19 @@ def test_decode_op_argument_checks_on_the_host():
     # 66 sub-chunks of 64 positions -> 33 workgroups of 2 per kv head
     ml = (8 * 33 * 5 * 2 * 4 + 255) // 256 * 256          # (max, sum) | partial outputs
     assert b.value == ml + 8 * 33 * 5 * 128 * 4
+    assert _status('wq_decode_attention_workspace_size', 32, 4, 128, 9000, ctypes.byref(b)) == _native.WQ_OK
+    ml = (4 * 47 * 8 * 2 * 4 + 255) // 256 * 256          # 141 sub-chunks -> 47 workgroups of 3
+    assert b.value == ml + 4 * 47 * 8 * 128 * 4
+    assert _status('wq_decode_attention_workspace_size', 40, 8, 128, 300, ctypes.byref(b)) == _native.WQ_OK
+    ml = (8 * 5 * 5 * 2 * 4 + 255) // 256 * 256           # 5 sub-chunks -> 5 workgroups of 1
+    assert b.value == ml + 8 * 5 * 5 * 128 * 4
     assert _status('wq_decode_attention_workspace_size', 40, 8, 64, 4224, ctypes.byref(b)) == _native.WQ_ERR_UNSUPPORTED
     assert b'head_dim 128' in _native.load().wq_last_error()
     assert _status('wq_decode_attention_workspace_size', 40, 3, 128, 4224, ctypes.byref(b)) == \
         _native.WQ_ERR_INVALID_ARGUMENT
     assert _status('wq_decode_attention_workspace_size', 80, 8, 128, 64, ctypes.byref(b)) == _native.WQ_ERR_UNSUPPORTED
-    assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 8192, ctypes.byref(b)) == _native.WQ_OK
-    assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 8193, ctypes.byref(b)) == \
+    assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 16384, ctypes.byref(b)) == _native.WQ_OK
+    assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 16385, ctypes.byref(b)) == \
         _native.WQ_ERR_UNSUPPORTED
     assert _status('wq_decode_attention_workspace_size', 8, 8, 128, 64, ctypes.byref(b)) == _native.WQ_OK
     assert b.value == 0        # one chunk: no cross-workgroup merge
