@@ -158,6 +158,25 @@ int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweig
 int wq_w8_quantize(const float* weight, int64_t n, int64_t k, int8_t* qweight, uint16_t* scale,
                    int32_t* status_flags, void* stream);
 
+/* W8A8, step 1: dynamic per-token symmetric INT8 quantization of the
+ * activations x fp16 [m, k] (k % 8 == 0): x_scale fp32 [m] =
+ * max(max_k |x[r, k]|, 1e-12) / 127 and qx int8 [m, k] =
+ * clamp(round_half_even(x / x_scale), -127, 127), an IEEE fp32 divide.
+ * Replaces vLLM's scaled_int8_quant(x, symmetric=True) in the int8_gemm
+ * backend (backend.py:252-253); the formula is the reference's W8A8 oracle
+ * (reference_w8a8, backend.py:258-261). */
+int wq_w8a8_quantize(const uint16_t* x, int64_t m, int64_t k, int8_t* qx, float* x_scale, void* stream);
+
+/* W8A8, step 2: y fp16 [m, n] = fp16(float(sum_k qx[m, k] * qweight[n, k])
+ * * x_scale[m] * w_scale[n] (+ bias[n])): int8 x int8 products summed
+ * exactly in int32 on the int8 matrix cores, scaled in fp32 in that order.
+ * qweight int8 [n, k] row-major (the compressed-tensors channel-INT8
+ * `weight`), w_scale fp32 [n]; k % 64 == 0, qx and qweight 16-byte aligned.
+ * Replaces vLLM's cutlass_scaled_mm(qx, qweight^T, x_scale, w_scale, fp16)
+ * (backend.py:254). */
+int wq_w8a8_linear(const int8_t* qx, const float* x_scale, int64_t m, int64_t k, const int8_t* qweight,
+                   const float* w_scale, int64_t n, const uint16_t* bias, uint16_t* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,8 @@ _SIGNATURES = {
     'wq_w8_decode': [_P, _P, _I64, _I64, _P, _P],
     'wq_w8a16_workspace_size': [_I64, _I64, _I64, _SIZE_P],
     'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
+    'wq_w8a8_quantize': [_P, _I64, _I64, _P, _P, _P],
+    'wq_w8a8_linear': [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P],
     'wq_w8_quantize': [_P, _I64, _I64, _P, _P, _P, _P],
     # include/ondeviceinfer_decode.h
     'wq_add_rmsnorm': [_P, _P, _P, _I64, _I64, ctypes.c_float, _P, _P, _P],
@@ -364,6 +366,47 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bi
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     _call('wq_w8a16_linear', _ptr(x), m, k, _ptr(q), _ptr(scale.contiguous()), n,
           _ptr(None if bias is None else bias.contiguous()), _ptr(out), ws_ptr, ws_bytes, _stream(device))
+    return out
+
+
+def w8a8_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dynamic per-token symmetric INT8: ``(qx int8 [m, k], x_scale fp32 [m])``
+    with ``x_scale = max(absmax, 1e-12) / 127`` (``wq_w8a8_quantize``)."""
+    device = _require_gpu(x)
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise TypeError(f'x must be a 2-D float16 tensor, got {x.dtype} {tuple(x.shape)}')
+    m, k = x.shape
+    x = _aligned(x.contiguous())
+    qx = torch.empty((m, k), dtype=torch.int8, device=device)
+    scale = torch.empty(m, dtype=torch.float32, device=device)
+    _call('wq_w8a8_quantize', _ptr(x), m, k, _ptr(qx), _ptr(scale), _stream(device))
+    return qx, scale
+
+
+def w8a8_linear(qx: torch.Tensor, x_scale: torch.Tensor, qweight: torch.Tensor, w_scale: torch.Tensor,
+                bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``y = fp16(float(qx . qweight^T) * x_scale[m] * w_scale[n] (+ bias))``,
+    int32 accumulation on the int8 matrix cores (``wq_w8a8_linear``)."""
+    device = _require_gpu(qx, x_scale, qweight, w_scale, bias, out)
+    if qx.dtype != torch.int8 or qx.dim() != 2 or qweight.dtype != torch.int8 or qweight.dim() != 2:
+        raise TypeError('qx and qweight must be 2-D INT8 tensors')
+    m, k = qx.shape
+    n = qweight.shape[0]
+    if qweight.shape[1] != k:
+        raise ValueError(f'input has {k} features, expected {qweight.shape[1]}')
+    _check(x_scale, torch.float32, (m,), 'x_scale')
+    if w_scale.dtype != torch.float32 or w_scale.numel() != n:
+        raise ValueError(f'w_scale must be float32 with {n} entries')
+    if bias is not None and (bias.dtype != torch.float16 or bias.numel() != n):
+        raise ValueError('bias must be FP16 with one entry per output feature')
+    qx = _aligned(qx.contiguous())
+    q = _aligned(qweight.contiguous())
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float16, device=device)
+    else:
+        _check(out, torch.float16, (m, n), 'out')
+    _call('wq_w8a8_linear', _ptr(qx), _ptr(x_scale.contiguous()), m, k, _ptr(q), _ptr(w_scale.contiguous()), n,
+          _ptr(None if bias is None else bias.contiguous()), _ptr(out), _stream(device))
     return out
 
 

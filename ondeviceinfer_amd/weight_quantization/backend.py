@@ -13,13 +13,16 @@ build's HIP library (``libondeviceinfer_wq.so``):
   (``wq_w4a16_linear``).
 * ``'w8a16'``: compressed-tensors channel INT8 (``weight`` int8 + ``weight_scale
   [N,1]``) as a weight-only fused INT8 x fp16 linear (``wq_w8a16_linear``).
-* ``'reference_int4'``: the explicit QDQ path, as in the reference: decode the
-  whole fp16 weight (``wq_w4_decode``/``wq_w8_decode``), then ``F.linear``.
+* ``'int8_gemm'``: W8A8 on compressed-tensors channel INT8: dynamic per-token
+  symmetric INT8 activations (``wq_w8a8_quantize``) times the INT8 weight,
+  int32 accumulation on the int8 matrix cores (``wq_w8a8_linear``), as the
+  reference's ``scaled_int8_quant`` + ``cutlass_scaled_mm`` (``backend.py:249-256``).
+* ``'reference_int4'`` / ``'reference_w8a8'``: the explicit QDQ paths, as in the
+  reference: decode the whole fp16 weight (``wq_w4_decode``/``wq_w8_decode``),
+  fake-quantize the activations per token for W8A8, then ``F.linear``.
 
 There is no silent fallback (``fallback_count`` stays 0): a missing library,
-an unsupported shape or a CPU tensor raises.  ``'int8_gemm'`` and
-``'reference_w8a8'`` (W8A8 with per-token activation quantization) are not
-built yet and raise ``ValueError`` naming the alternative.
+an unsupported shape or a CPU tensor raises.
 """
 from __future__ import annotations
 
@@ -37,11 +40,8 @@ from ..config import Qwen3Config
 from ..profiling import nvtx_range
 from ..runtime.quantized import LINEAR_WEIGHT_NAMES, NORM_WEIGHT_NAMES
 
-BACKEND_NAMES = ('marlin', 'w8a16', 'reference_int4')
-NOT_BUILT = {
-    'int8_gemm': "W8A8 'int8_gemm' is not built in this version; use 'w8a16' for weight-only INT8",
-    'reference_w8a8': "'reference_w8a8' is not built in this version; use 'reference_int4'",
-}
+BACKEND_NAMES = ('marlin', 'int8_gemm', 'w8a16', 'reference_int4', 'reference_w8a8')
+FUSED_BACKENDS = ('marlin', 'int8_gemm', 'w8a16')
 
 
 def unpack_unsigned(packed: torch.Tensor, bits: int, axis: int, length: int) -> torch.Tensor:
@@ -99,6 +99,13 @@ class PreparedW8(NamedTuple):
     n: int
 
 
+class PreparedW8A8(NamedTuple):
+    qweight: torch.Tensor     # int8 [N, K] (row-major, consumed as stored)
+    scale: torch.Tensor       # fp32 [N]
+    k: int
+    n: int
+
+
 class NativeOps:
     """Tensor-level calls into the HIP library; swappable for tests (the
     reference's own dispatch test swaps ``backend.ops`` the same way)."""
@@ -111,6 +118,15 @@ class NativeOps:
     @staticmethod
     def w8a16_linear(x: torch.Tensor, prepared: PreparedW8, output: torch.Tensor | None = None) -> torch.Tensor:
         return _native.w8a16_linear(x, prepared.qweight, prepared.scale, out=output)
+
+    @staticmethod
+    def w8a8_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        return _native.w8a8_quantize(x)
+
+    @staticmethod
+    def w8a8_linear(qx: torch.Tensor, x_scale: torch.Tensor, prepared: PreparedW8A8,
+                    output: torch.Tensor | None = None) -> torch.Tensor:
+        return _native.w8a8_linear(qx, x_scale, prepared.qweight, prepared.scale, out=output)
 
 
 @dataclass
@@ -261,8 +277,6 @@ class CompressedLinearBackend:
     """Same surface as the reference backend (``backend.py:172-263``)."""
 
     def __init__(self, name: str, group_size: int = 128):
-        if name in NOT_BUILT:
-            raise ValueError(NOT_BUILT[name])
         if name not in BACKEND_NAMES:
             raise ValueError(name)
         self.name, self.group_size = name, group_size
@@ -276,7 +290,7 @@ class CompressedLinearBackend:
         # Recorded for report compatibility; these kernels always reduce in fp32.
         self.marlin_use_fp32_reduce = os.environ.get('ONDEVICEINFER_MARLIN_FP32_REDUCE', '0') == '1'
         self.ops = NativeOps()
-        if name in ('marlin', 'w8a16'):
+        if name in FUSED_BACKENDS:
             _native.load()   # fail at construction, like the reference's vLLM import
 
     # -- fused dispatch (the reference's _marlin_gemm, backend.py:195-202)
@@ -284,6 +298,10 @@ class CompressedLinearBackend:
         self.gemm_calls += 1
         if isinstance(prepared, PreparedW8):
             return self.ops.w8a16_linear(x, prepared, output)
+        if isinstance(prepared, PreparedW8A8):
+            qx, x_scale = self.ops.w8a8_quantize(x)
+            self.activation_quantize_calls += 1
+            return self.ops.w8a8_linear(qx, x_scale, prepared, output)
         return self.ops.w4a16_linear(x, prepared, output)
 
     def prepare(self, layer: dict, name: str) -> None:
@@ -303,13 +321,17 @@ class CompressedLinearBackend:
             # The fused path retains only the repacked weights (backend.py:224-226).
             for suffix in ('.weight_packed', '.weight_scale', '.weight_zero_point'):
                 layer.pop(prefix + suffix, None)
-        elif self.name == 'w8a16':
+        elif self.name in ('w8a16', 'int8_gemm'):
             q = layer[name]
             if q.dtype != torch.int8:
                 raise TypeError(f'{name}: expected INT8, got {q.dtype}')
             n, k = q.shape
-            scale = layer[prefix + '.weight_scale'].reshape(-1).half().contiguous()
-            layer[prefix + '._prepared'] = PreparedW8(q.contiguous(), scale, k, n)
+            if self.name == 'w8a16':
+                scale = layer[prefix + '.weight_scale'].reshape(-1).half().contiguous()
+                layer[prefix + '._prepared'] = PreparedW8(q.contiguous(), scale, k, n)
+            else:   # the reference keeps the scale in fp32 for the scaled GEMM (backend.py:231)
+                scale = layer[prefix + '.weight_scale'].float().reshape(-1).contiguous()
+                layer[prefix + '._prepared'] = PreparedW8A8(q.contiguous(), scale, k, n)
 
     def fuse_projections(self, layer: dict) -> None:
         """Add ``self_attn.qkv_proj._prepared`` and ``mlp.gate_up_proj._prepared``:
@@ -339,24 +361,25 @@ class CompressedLinearBackend:
                                                             meta=meta[m0:m0 + p.meta.numel()])
                     t0 += p.tiles.numel()
                     m0 += p.meta.numel()
-            elif all(isinstance(p, PreparedW8) for p in preps):
+            elif all(isinstance(p, PreparedW8) for p in preps) or all(isinstance(p, PreparedW8A8) for p in preps):
                 if len({p.k for p in preps}) != 1:
                     continue
+                kind = type(preps[0])
                 q = torch.cat([p.qweight for p in preps])
                 sc = torch.cat([p.scale for p in preps])
-                layer[fused + '._prepared'] = PreparedW8(q, sc, preps[0].k, int(q.shape[0]))
+                layer[fused + '._prepared'] = kind(q, sc, preps[0].k, int(q.shape[0]))
                 r0 = 0
                 for part, p in zip(parts, preps):
-                    layer[part + '._prepared'] = PreparedW8(q[r0:r0 + p.n], sc[r0:r0 + p.n], p.k, p.n)
+                    layer[part + '._prepared'] = kind(q[r0:r0 + p.n], sc[r0:r0 + p.n], p.k, p.n)
                     r0 += p.n
 
     def linear(self, inputs: torch.Tensor, weights: dict, name: str) -> torch.Tensor:
         self.calls += 1
         prefix = name.removesuffix('.weight')
         with nvtx_range(f'weight_quant::{self.name}::{name}'):
-            if self.name in ('marlin', 'w8a16'):
+            if self.name in FUSED_BACKENDS:
                 prepared = weights[prefix + '._prepared']
-                k, n = prepared[-2:] if isinstance(prepared, PreparedW8) else (prepared.k, prepared.n)
+                k, n = prepared.k, prepared.n
                 x = inputs.reshape(-1, k).contiguous()
                 if self.marlin_max_rows_per_call <= 0 or x.shape[0] <= self.marlin_max_rows_per_call:
                     out = self._fused(x, prepared)
@@ -368,4 +391,9 @@ class CompressedLinearBackend:
                 return out.reshape(*inputs.shape[:-1], n)
             weight = decode_weight(weights, name, group_size=self.group_size)
             self.explicit_dequant_bytes += weight.numel() * weight.element_size()
+            if self.name == 'reference_w8a8':
+                # Per-token symmetric fake quantization (backend.py:258-261).
+                x = inputs.float()
+                scale = x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12) / 127
+                inputs = (x.div(scale).round().clamp(-127, 127) * scale).half()
             return F.linear(inputs, weight)

@@ -26,6 +26,15 @@ quantize_linear_weight     reference invariants ``tests/test_quantization.py:21-
                            stored-scale use and the fp16 underflow rule
 dequantize_linear_weight   reference KAT ``test_weight_quant_backend.py:33-35``
 linear_fp32                float64 brute-force loop on small non-square shapes
+quantize_activations_      hand-derived vectors (round-half-even ties at scale
+  per_token                1, the fp32 scale bits, the 1e-12 floor of a zero
+                           row); the reference's torch expression
+                           (``backend.py:258-260``) evaluated on the CPU
+reference_w8a8_linear      the reference's torch lines (``backend.py:257-263``)
+                           evaluated on the CPU (amax/div/round/clamp, F.linear
+                           in fp32)
+w8a8_linear_int            Python-integer brute force + float32 scaling on
+                           small shapes
 parity_metrics             closed-form values on hand-made vectors
 =========================  ====================================================
 """
@@ -211,6 +220,44 @@ def int8_weight_only_linear(x: np.ndarray, qweight: np.ndarray, scale: np.ndarra
     """INT8 explicit path, restating ``quantized_model.py:76-121``: dequantize
     into fp16 then ``F.linear``."""
     return linear_fp32(x, dequantize_linear_weight(qweight, scale))
+
+
+def quantize_activations_per_token(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-token symmetric INT8 of the ``reference_w8a8`` backend
+    (``backend.py:258-260``): in fp32, ``scale = max(absmax_row, 1e-12) / 127``,
+    ``q = clamp(round(x / scale), -127, 127)`` with round-half-even.  Returns
+    ``(q int8 [M, K], scale fp32 [M])``; the reference multiplies them back
+    (``* scale``) before its fp16 linear."""
+    x32 = np.asarray(x).astype(np.float32)
+    absmax = np.abs(x32).max(axis=-1, keepdims=True)
+    scale = (np.maximum(absmax, np.float32(1e-12)) / np.float32(127)).astype(np.float32)
+    q = np.clip(np.rint(x32 / scale), QMIN, QMAX).astype(np.int8)
+    return q, scale[..., 0]
+
+
+def reference_w8a8_linear(x: np.ndarray, qweight: np.ndarray, w_scale: np.ndarray) -> np.ndarray:
+    """The ``reference_w8a8`` backend (``backend.py:257-263``): the channel-INT8
+    weight decoded to fp16 (``decode_weight``, ``:37-40``), the activations
+    fake-quantized per token (``q * scale`` rounded to fp16), then ``F.linear``."""
+    q, s = quantize_activations_per_token(x)
+    xq = (q.astype(np.float32) * s[:, None]).astype(np.float16)
+    return linear_fp32(xq, dequantize_linear_weight(qweight, w_scale))
+
+
+def w8a8_linear_int(qx: np.ndarray, x_scale: np.ndarray, qweight: np.ndarray, w_scale: np.ndarray,
+                    bias: np.ndarray | None = None) -> np.ndarray:
+    """The ``int8_gemm`` backend's scaled INT8 GEMM (vLLM ``cutlass_scaled_mm``,
+    called at ``backend.py:254``): the int8 x int8 products summed exactly, then
+    ``fp16(float(acc) * x_scale[m] * w_scale[n] (+ bias[n]))`` in fp32, left to
+    right.  vLLM (``vllm==0.12.0``) is absent here; this restates the published
+    semantics of a scaled int8 matmul (exact integer accumulation, one fp32
+    rescale) and is pinned by brute force on small shapes."""
+    acc = np.asarray(qx).astype(np.int64) @ np.asarray(qweight).astype(np.int64).T
+    y = acc.astype(np.float32) * np.asarray(x_scale).astype(np.float32)[:, None]
+    y = y * np.asarray(w_scale).astype(np.float32).reshape(1, -1)
+    if bias is not None:
+        y = y + np.asarray(bias).astype(np.float32).reshape(1, -1)
+    return y.astype(np.float16)
 
 
 def parity_metrics(actual: np.ndarray, expected: np.ndarray) -> dict:

@@ -26,11 +26,40 @@ KAT = json.loads((Path(__file__).parent / 'golden' / 'weight_quant_kat.json').re
 def test_backend_names():
     with pytest.raises(ValueError):
         wq.CompressedLinearBackend('bogus')
-    for name in ('int8_gemm', 'reference_w8a8'):
-        with pytest.raises(ValueError, match='not built'):
-            wq.CompressedLinearBackend(name)
-    b = wq.CompressedLinearBackend('reference_int4')
-    assert (b.calls, b.gemm_calls, b.fallback_count, b.explicit_dequant_bytes) == (0, 0, 0, 0)
+    for name in ('reference_int4', 'reference_w8a8', 'int8_gemm', 'w8a16', 'marlin'):
+        b = wq.CompressedLinearBackend(name)
+        assert (b.calls, b.gemm_calls, b.fallback_count, b.explicit_dequant_bytes,
+                b.activation_quantize_calls) == (0, 0, 0, 0, 0)
+
+
+def test_int8_gemm_prepare_and_dispatch():
+    """``prepare`` keeps the INT8 weight as stored with an fp32 scale
+    (``backend.py:227-231``); ``linear`` quantizes the activations once and
+    runs one scaled INT8 GEMM per call, counting both (``:249-256``)."""
+    backend = wq.CompressedLinearBackend('int8_gemm')
+    q = torch.randint(-127, 128, (24, 64), dtype=torch.int8)
+    layer = {'mlp.up_proj.weight': q, 'mlp.up_proj.weight_scale': torch.rand(24, 1).half()}
+    backend.prepare(layer, 'mlp.up_proj.weight')
+    p = layer['mlp.up_proj._prepared']
+    assert isinstance(p, wq.PreparedW8A8) and (p.k, p.n) == (64, 24)
+    assert p.scale.dtype == torch.float32 and p.scale.shape == (24,) and torch.equal(p.qweight, q)
+    seen = []
+
+    def fake_quant(x):
+        seen.append(('quant', tuple(x.shape)))
+        return x.round().to(torch.int8), torch.ones(x.shape[0])
+
+    def fake_linear(qx, sx, prepared, output=None):
+        seen.append(('gemm', tuple(qx.shape)))
+        return qx.float().half() @ prepared.qweight.t().float().half()
+
+    backend.ops = SimpleNamespace(w8a8_quantize=fake_quant, w8a8_linear=fake_linear)
+    out = backend.linear(torch.randn(2, 3, 64), layer, 'mlp.up_proj.weight')
+    assert out.shape == (2, 3, 24)
+    assert seen == [('quant', (6, 64)), ('gemm', (6, 64))]
+    assert (backend.calls, backend.gemm_calls, backend.activation_quantize_calls) == (1, 1, 1)
+    with pytest.raises(TypeError, match='expected INT8'):
+        backend.prepare({'x.weight': q.float(), 'x.weight_scale': torch.ones(24, 1)}, 'x.weight')
 
 
 def test_row_split_dispatch_preserves_shape_and_counts():

@@ -244,3 +244,71 @@ def test_awq_synthetic_quantizer_is_valid_and_close():
     # round-to-nearest: half a step, plus the fp16 rounding of the decoded value
     w32 = w.astype(np.float32)
     assert np.all(np.abs(dec - w32) <= s * 0.5 + np.abs(w32) * 2.0 ** -10 + 1e-7)
+
+
+# ------------------------------------------------------------------- W8A8
+def test_w8a8_activation_quantizer_known_answers():
+    """Hand-derived: at absmax 127 the scale is exactly 1, so x / scale = x
+    and the ties 62.5 / -2.5 / 0.5 show round-half-even (62, -2, 0; half-away
+    would give 63, -3, 1); a zero row takes the 1e-12 floor (q = 0, scale
+    bits of fp32(1e-12) / 127); the scale of absmax 1 is the fp32 quotient
+    1/127, not its fp16 rounding."""
+    x = np.array([[127.0, 62.5, -2.5, 0.5, -127.0, 3.0, 0.0, 1.0],
+                  [0.0] * 8,
+                  [1.0, -0.5, 0.25, 0.0, 0.0, 0.0, 0.0, 0.0]], dtype=np.float16)
+    q, s = qdq.quantize_activations_per_token(x)
+    assert q.dtype == np.int8 and s.dtype == np.float32
+    assert q[0].tolist() == [127, 62, -2, 0, -127, 3, 0, 1]
+    assert s[0] == np.float32(1.0)
+    assert q[1].tolist() == [0] * 8 and s[1] == np.float32(np.float32(1e-12) / np.float32(127))
+    assert s[2] == np.float32(1.0) / np.float32(127) and s[2] != np.float32(np.float16(1.0 / 127))
+    assert q[2].tolist() == [127, -64, 32, 0, 0, 0, 0, 0]   # -63.5 -> -64 and 31.75 -> 32
+
+
+def test_w8a8_activation_quantizer_matches_reference_torch_expression():
+    """The reference's own torch lines (backend.py:258-260) on the CPU."""
+    import torch
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((7, 96)) * rng.choice([0.01, 1.0, 30.0], size=(7, 1))).astype(np.float16)
+    x[3] = 0
+    t = torch.from_numpy(x).float()
+    scale = t.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12) / 127
+    q_ref = t.div(scale).round().clamp(-127, 127)
+    q, s = qdq.quantize_activations_per_token(x)
+    assert np.array_equal(q.astype(np.float32), q_ref.numpy())
+    assert np.array_equal(s, scale.numpy()[:, 0])
+
+
+def test_reference_w8a8_linear_matches_reference_torch_lines():
+    """backend.py:257-263 on the CPU: decode the channel-INT8 weight, fake
+    quantize x, F.linear (fp32 accumulation)."""
+    import torch
+    import torch.nn.functional as F
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((5, 64)).astype(np.float16)
+    qw = rng.integers(-127, 128, (12, 64)).astype(np.int8)
+    ws = (rng.random(12) * 0.01 + 1e-3).astype(np.float16)
+    t = torch.from_numpy(x).float()
+    scale = t.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12) / 127
+    xq = (t.div(scale).round().clamp(-127, 127) * scale).half()
+    w = (torch.from_numpy(qw).float() * torch.from_numpy(ws).float()[:, None]).half()
+    expected = F.linear(xq.float(), w.float()).half().numpy()
+    assert np.array_equal(qdq.reference_w8a8_linear(x, qw, ws), expected)
+
+
+def test_w8a8_scaled_int_gemm_brute_force():
+    """Python-integer dot products, then the fp32 scaling left to right."""
+    rng = np.random.default_rng(7)
+    qx = rng.integers(-127, 128, (3, 40)).astype(np.int8)
+    qw = rng.integers(-127, 128, (5, 40)).astype(np.int8)
+    xs = (rng.random(3) * 0.1).astype(np.float32)
+    wsc = (rng.random(5) * 0.01).astype(np.float32)
+    bias = rng.standard_normal(5).astype(np.float16)
+    got = qdq.w8a8_linear_int(qx, xs, qw, wsc, bias)
+    for m in range(3):
+        for n in range(5):
+            acc = sum(int(qx[m, k]) * int(qw[n, k]) for k in range(40))
+            r = np.float32(np.float32(np.float32(acc) * xs[m]) * wsc[n]) + np.float32(bias[n])
+            assert got[m, n] == np.float16(np.float32(r))
+    # the largest magnitude a Qwen3 shape produces still fits int32
+    assert 127 * 127 * 17408 < 2 ** 31
