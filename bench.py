@@ -6,9 +6,11 @@ quoted on): batch 1, a 4096-token random prompt, greedy decode with the fp16
 KV cache resident, random-init weights of the Qwen3-14B architecture (40
 layers, hidden 5120, 40/8 heads of 128, SwiGLU 17408, vocab 151936), the
 decoder linears uint4 with fp16 group-128 scales and zero points.  One *step*
-is one decode token: a replay of the captured decode-step graph (40 x [add +
-RMSNorm, fused QKV GEMV, fused attention kernel, o GEMV, add + RMSNorm, fused
-gate_up GEMV, SiLU*up, down GEMV], final norm, fp16 LM head) plus the argmax.
+is one decode token: a replay of the captured decode-step graph (40 x [QKV
+GEMV with the input RMSNorm in its prologue, attention (q/k norm, RoPE, cache
+append, GQA) + chunk merge, o GEMV + residual, gate_up GEMV with the
+post-attention RMSNorm in its prologue, down GEMV with SiLU*up in its prologue
++ residual], final norm, fp16 LM head) plus the argmax.
 After the prefill and ``--warmup`` untimed steps, ``--steps`` steps are timed;
 ``value`` = steps / seconds (tok/s), compared with the reference's published
 26.358 tok/s (AWQ-INT4 + Marlin, RTX 3090, same workload).
@@ -23,6 +25,8 @@ Also in the same JSON line:
   they run on; ``traffic`` from the committed rocprofv3 counter summary;
 * ``decode_step_kernels``: the same timing for every kernel of the step;
 * ``prefill``: the M=4096 W4A16 GEMM (configs[2]) per shape, TFLOP/s;
+* ``int8``: configs[0]'s INT8 weight on the GPU: weight-only W8A16 decode GB/s,
+  and W8A8 (``int8_gemm``) decode GB/s and M=4096 TOPS vs the int8 MFMA peak;
 * ``copy_ceiling``: a device-to-device copy's GB/s on the same box;
 * ``cpu_baseline``: the numpy QDQ oracle on one decoder layer's decode work,
   scaled to tok/s for the 40-layer model.
@@ -43,6 +47,7 @@ METRIC = 'Qwen3-14B AWQ-INT4 decode tok/s at B=1; W4A16 GEMV % of HBM peak'
 PUBLISHED_TOKS = 26.358          # AWQ INT4 G=128 + vLLM Marlin, RTX 3090, same workload
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+INT8_MFMA_PEAK_TOPS = 5000.0      # dense int8 MFMA, MI355X
 GROUP = 128
 PROMPT = 4096
 HIDDEN, INTER, KV, QKV, GATE_UP = 5120, 17408, 1024, 7168, 34816
@@ -390,6 +395,49 @@ def main() -> int:
                             'tflops': round(tflops, 1), 'frac_fp16_mfma': round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)})
             del g, yp
         result['prefill'] = prefill
+
+        # INT8 variants on configs[0]'s weight (5120 x 5120, N(0, 0.02), per-channel
+        # symmetric INT8): weight-only W8A16 decode, and W8A8 (int8_gemm) decode
+        # and M=4096 prefill on the int8 matrix cores.
+        g0 = torch.Generator(device=device).manual_seed(0)
+        w8 = (torch.randn(HIDDEN, HIDDEN, device=device, generator=g0) * 0.02).float()
+        q8w, s8w = native.w8_quantize(w8)
+        s8w32 = s8w.float()
+        del w8
+        int8 = []
+        x1 = torch.randn(1, HIDDEN, device=device).half()
+        x4k = torch.randn(4096, HIDDEN, device=device).half()
+        qx1, sx1 = native.w8a8_quantize(x1)
+        qx4k, sx4k = native.w8a8_quantize(x4k)
+        y1 = torch.empty(1, HIDDEN, device=device, dtype=torch.float16)
+        y4k = torch.empty(4096, HIDDEN, device=device, dtype=torch.float16)
+        cases = [
+            ('w8a16 decode (configs[0] on the GPU)', 1, lambda: native.w8a16_linear(x1, q8w, s8w, out=y1)),
+            ('w8a8 int8_gemm decode (quantize + linear)', 1,
+             lambda: native.w8a8_linear(*native.w8a8_quantize(x1), q8w, s8w32, out=y1)),
+            ('w8a8 linear only, decode', 1, lambda: native.w8a8_linear(qx1, sx1, q8w, s8w32, out=y1)),
+            ('w8a8 linear only, prefill M=4096', 4096, lambda: native.w8a8_linear(qx4k, sx4k, q8w, s8w32, out=y4k)),
+        ]
+        for label, mm, fn in cases:
+            fn()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(10):
+                    fn()
+            sec = time_graph(torch, g, 10) / 10
+            w8a8 = 'w8a8' in label   # int8 x and fp32 scales vs fp16 x and fp16 scales
+            b = HIDDEN * HIDDEN + (4 if w8a8 else 2) * HIDDEN + (1 if w8a8 else 2) * mm * HIDDEN + 2 * mm * HIDDEN
+            entry = {'op': label, 'shape': f'{HIDDEN}->{HIDDEN}', 'M': mm, 'us': round(sec * 1e6, 2)}
+            if mm == 1:
+                entry.update(gbs=round(b / sec / 1e9, 1), frac_hbm=round(b / sec / 1e9 / HBM_PEAK_GBS, 4),
+                             algorithmic_bytes=b)
+            else:
+                tops = 2 * mm * HIDDEN * HIDDEN / sec / 1e12
+                entry.update(tops=round(tops, 1), frac_int8_mfma=round(tops / INT8_MFMA_PEAK_TOPS, 4))
+            int8.append(entry)
+            del g
+        result['int8'] = int8
+        del q8w, s8w, s8w32, x4k, qx4k, y4k
 
         # Copy ceiling: 2 GiB device-to-device copy (read + write bytes).
         src = torch.empty(2**30, dtype=torch.uint16, device=device)

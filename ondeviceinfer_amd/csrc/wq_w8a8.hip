@@ -121,68 +121,128 @@ __global__ __launch_bounds__(1024) void w8a8_gemv_kernel(const int8_t* __restric
   }
 }
 
-// M > 16: grid = (ceil(N / 64), ceil(M / 64)), 256 threads.  Wave w owns the
-// 16 weight rows 64*bx + 16w .. +15; the four waves share the 64 x rows
-// 64*by .. +63 (four 16-column blocks, so every weight fragment feeds four
-// MFMAs; the x fragments are L1 hits for three of the four waves).  K is
-// walked in chunks of four 64-k steps, the next chunk requested before the
-// current one is multiplied.
-constexpr int kGemmChunk = 4;
+// 16 bytes per lane global -> LDS (global_load_lds_dwordx4): lane L's bytes
+// land at lds_base + 16 * L.  Kept out of the kernel template: with the
+// builtin written inside it, the host pass drops the kernel's launch stub.
+__device__ __forceinline__ void i8_lds_load16(const void* src, uint8_t* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
 
-__global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restrict__ qx,
+// LDS slot of 16-byte chunk c (0..7) in row r of a 128-byte stage row: rows
+// 2 apart share banks, so the slot is permuted by r / 2; the sixteen rows a
+// B-fragment read touches then hit sixteen distinct 16-byte bank groups.
+__device__ __forceinline__ int i8_swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+constexpr int kI8Blk = 128;              // k per GEMM stage (two int8 MFMA steps)
+constexpr int kI8RowBytes = kI8Blk;      // one int8 x row per stage
+
+// M > 16: grid = (ceil(tiles / (4 NT)), ceil(M / BM)), 256 threads, BM = 16 MT.
+// Wave w owns the NT 16-row weight tiles (4 bx + w) NT .. +NT-1 (disjoint
+// between waves); all four share the BM x rows of the workgroup.  Per 128-k
+// stage the x tile goes global -> LDS with global_load_lds_dwordx4 into a
+// two-stage ring (row r's chunk c at slot i8_swz(r, c)); each wave's weight
+// fragments come straight from memory into registers one stage ahead.  Per
+// 64-k step a wave reads MT x fragments from LDS and issues NT x MT int8
+// MFMAs.  K % 128 == 0.
+template <int NT, int MT>
+__global__ __launch_bounds__(256, 1) void w8a8_gemm_kernel(const int8_t* __restrict__ qx,
                                                            const float* __restrict__ sx, int M, int K,
                                                            const int8_t* __restrict__ qw,
                                                            const float* __restrict__ sw,
                                                            const half_t* __restrict__ bias, int N,
                                                            half_t* __restrict__ y) {
-  constexpr int CH = kGemmChunk;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, kb = lane >> 4;
-  const int n0 = blockIdx.x * 64 + wave * 16, m0 = blockIdx.y * 64;
-  const int nsteps = K / kI8Step;   // a multiple of CH (checked by the host)
-  const int8_t* wp = qw + (size_t)min(n0 + i, N - 1) * K + 16 * kb;
-  const int8_t* xp[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) xp[j] = qx + (size_t)min(m0 + 16 * j + i, M - 1) * K + 16 * kb;
-  int4v_t acc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = int4v_t{0, 0, 0, 0};
+  constexpr int BM = MT * 16;
+  constexpr int kStageBytes = BM * kI8RowBytes;
+  constexpr int kInstrPerWave = kStageBytes / 1024 / 4;   // 1 KiB per wave-wide DMA instruction
+  static_assert(kInstrPerWave >= 1, "stage too small for four waves");
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[2 * kStageBytes];
 
-  uint4_t a[CH], b[CH][4];
-  auto load_chunk = [&](int c, uint4_t (&aa)[CH], uint4_t (&bb)[CH][4]) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 15, kb = lane >> 4;
+  const int ntile = (N + 15) >> 4;
+  const int nblk = K / kI8Blk;
+  const int m0 = blockIdx.y * BM;
+  const int tile0 = ((int)blockIdx.x * 4 + wave) * NT;
+  const int8_t* wrow[NT];
 #pragma unroll
-    for (int t = 0; t < CH; ++t) {
-      const size_t off = (size_t)kI8Step * (c * CH + t);
-      aa[t] = *reinterpret_cast<const uint4_t*>(wp + off);   // cached: every 64 rows of x reread it
+  for (int t = 0; t < NT; ++t) wrow[t] = qw + (size_t)min(min(tile0 + t, ntile - 1) * 16 + i, N - 1) * K + 16 * kb;
+
+  // Stage `st` <- x rows m0 .. m0+BM-1, k block `blk`: instruction J of the
+  // workgroup fills bytes [1024 J, 1024 J + 1024), i.e. rows 8J .. 8J+7;
+  // lane L lands in row 8J + L/8, slot L%8, so it fetches chunk
+  // i8_swz(row, L%8) of that row.
+  auto copy_x = [&](int blk, int st) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bb[t][j] = *reinterpret_cast<const uint4_t*>(xp[j] + off);
+    for (int j = 0; j < kInstrPerWave; ++j) {
+      const int J = wave * kInstrPerWave + j;
+      const int r = 8 * J + (lane >> 3);
+      const int c = i8_swz(r, lane & 7);
+      const int8_t* src = qx + (size_t)min(m0 + r, M - 1) * K + (size_t)blk * kI8Blk + 16 * c;
+      i8_lds_load16(src, xs + st * kStageBytes + J * 1024);
     }
   };
-  const int nchunks = nsteps / CH;
-  load_chunk(0, a, b);
-  for (int c = 0; c < nchunks; ++c) {
-    uint4_t an[CH], bn[CH][4];
-    if (c + 1 < nchunks) load_chunk(c + 1, an, bn);
+  auto fetch_w = [&](int blk, uint4_t (&r)[NT][2]) {
 #pragma unroll
-    for (int t = 0; t < CH; ++t)
+    for (int t = 0; t < NT; ++t) {
+      const uint4_t* p = reinterpret_cast<const uint4_t*>(wrow[t] + (size_t)blk * kI8Blk);
+      r[t][0] = p[0];   // k + 16 kb .. +15
+      r[t][1] = p[4];   // k + 64 + 16 kb .. +15
+    }
+  };
+
+  int4v_t acc[NT][MT];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = mfma_i8(a[t], b[t][j], acc[j]);
-    if (c + 1 < nchunks) {
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int t = 0; t < CH; ++t) {
-        a[t] = an[t];
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = int4v_t{0, 0, 0, 0};
+
+  uint4_t cur[NT][2], nxt[NT][2];
+  copy_x(0, 0);
+  fetch_w(0, cur);
+  __builtin_amdgcn_s_waitcnt(0);   // stage 0 landed
+  __syncthreads();
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int st = blk & 1;
+    const bool more = blk + 1 < nblk;
+    if (more) {
+      copy_x(blk + 1, st ^ 1);
+      fetch_w(blk + 1, nxt);
+    }
+    const uint8_t* stage = xs + st * kStageBytes;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[t][j] = bn[t][j];
+    for (int step = 0; step < 2; ++step) {
+      const int c = 4 * step + kb;   // 16-byte chunk of this lane's k range
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int r = mt * 16 + i;
+        const uint4_t b = *reinterpret_cast<const uint4_t*>(stage + r * kI8RowBytes + i8_swz(r, c) * 16);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b, acc[t][mt]);
       }
     }
-  }
+    if (more) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + 16 * j + i;
-    if (m < M) {
+      for (int t = 0; t < NT; ++t) {
+        cur[t][0] = nxt[t][0];
+        cur[t][1] = nxt[t][1];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's part of the next stage landed
+    __syncthreads();                  // ... and everyone's; stage st may be overwritten next
+  }
+
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (tile0 + t >= ntile) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 16 + i;
+      if (m >= M) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int n = n0 + 4 * kb + v;
-        if (n < N) w8a8_store(acc[j][v], m, n, sx, sw, bias, N, y);
+        const int n = (tile0 + t) * 16 + 4 * kb + v;
+        if (n < N) w8a8_store(acc[t][mt][v], m, n, sx, sw, bias, N, y);
       }
     }
   }
@@ -217,27 +277,36 @@ extern "C" int wq_w8a8_linear(const int8_t* qx, const float* x_scale, int64_t m,
              "qx and qweight must be 16-byte aligned");
   const half_t* b = reinterpret_cast<const half_t*>(bias);
   half_t* yy = reinterpret_cast<half_t*>(y);
-  if (m <= kW8A8GemvMaxM || (k / kI8Step) % kGemmChunk != 0) {
-    const int64_t nsteps = k / kI8Step, ntile = (n + 15) / 16;
-    int ksw = (int)((nsteps + 9) / 10);
-    ksw = ksw < 1 ? 1 : (ksw > 16 ? 16 : ksw);
-    if (m > kW8A8GemvMaxM) {
-      // k/64 not a multiple of the GEMM chunk: run the decode kernel per 16 rows of x.
-      for (int64_t r = 0; r < m; r += kW8A8GemvMaxM) {
-        const int64_t mr = m - r < kW8A8GemvMaxM ? m - r : kW8A8GemvMaxM;
-        hipLaunchKernelGGL(w8a8_gemv_kernel, dim3((unsigned)ntile), dim3(64 * ksw), 0, as_stream(stream),
-                           qx + r * k, x_scale + r, (int)mr, (int)k, qweight, w_scale, b, (int)n, yy + r * n);
-        const int rc = check_launch("w8a8_gemv");
-        if (rc != WQ_OK) return rc;
-      }
-      return WQ_OK;
+  const int64_t nsteps = k / kI8Step, ntile = (n + 15) / 16;
+  if (m > kW8A8GemvMaxM && k % kI8Blk == 0) {
+    // GEMM: 128-row x tiles for long batches, 32-row ones otherwise; four
+    // weight tiles per wave while that still leaves a full machine of
+    // workgroups, else one.
+    const bool big_m = m >= 256;
+    const int64_t mblocks = big_m ? (m + 127) / 128 : (m + 31) / 32;
+    const int nt = (ntile + 15) / 16 * mblocks >= 256 ? 4 : 1;
+    WQ_REQUIRE(mblocks <= 65535, WQ_ERR_UNSUPPORTED, "too many rows for the W8A8 GEMM grid");
+    const dim3 grid((unsigned)((ntile + 4 * nt - 1) / (4 * nt)), (unsigned)mblocks);
+    auto launch = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, dim3(256), 0, as_stream(stream), qx, x_scale, (int)m, (int)k, qweight,
+                         w_scale, b, (int)n, yy);
+    };
+    if (big_m) {
+      if (nt == 4) launch(w8a8_gemm_kernel<4, 8>); else launch(w8a8_gemm_kernel<1, 8>);
+    } else {
+      if (nt == 4) launch(w8a8_gemm_kernel<4, 2>); else launch(w8a8_gemm_kernel<1, 2>);
     }
-    hipLaunchKernelGGL(w8a8_gemv_kernel, dim3((unsigned)ntile), dim3(64 * ksw), 0, as_stream(stream), qx, x_scale,
-                       (int)m, (int)k, qweight, w_scale, b, (int)n, yy);
-    return check_launch("w8a8_gemv");
+    return check_launch("w8a8_gemm");
   }
-  WQ_REQUIRE((m + 63) / 64 <= 65535, WQ_ERR_UNSUPPORTED, "too many rows for the W8A8 GEMM grid");
-  hipLaunchKernelGGL(w8a8_gemm_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64)), dim3(256), 0,
-                     as_stream(stream), qx, x_scale, (int)m, (int)k, qweight, w_scale, b, (int)n, yy);
-  return check_launch("w8a8_gemm");
+  // Decode kernel: about eight 64-k steps per wave (one round of loads).
+  int ksw = (int)((nsteps + 7) / 8);
+  ksw = ksw < 1 ? 1 : (ksw > 16 ? 16 : ksw);
+  for (int64_t r = 0; r < m; r += kW8A8GemvMaxM) {   // batches beyond 16 rows only when k % 128 != 0
+    const int64_t mr = m - r < kW8A8GemvMaxM ? m - r : kW8A8GemvMaxM;
+    hipLaunchKernelGGL(w8a8_gemv_kernel, dim3((unsigned)ntile), dim3(64 * ksw), 0, as_stream(stream), qx + r * k,
+                       x_scale + r, (int)mr, (int)k, qweight, w_scale, b, (int)n, yy + r * n);
+    const int rc = check_launch("w8a8_gemv");
+    if (rc != WQ_OK) return rc;
+  }
+  return WQ_OK;
 }

@@ -51,7 +51,8 @@ def test_w8a8_quantize_bit_exact(m, k, scale):
     (17, 80, 256, False),        # smallest GEMM batch, ragged m and n
     (65, 1000, 5120, True),
     (300, 520, 192, False),      # GEMM batch with k/64 not a multiple of the chunk -> decode kernel per 16 rows
-    (256, 5120, 5120, False),
+    (256, 5120, 5120, False),    # GEMM, 128-row x tiles, one weight tile per wave
+    (200, 17408, 128, True),     # GEMM, 32-row x tiles, four weight tiles per wave
 ])
 def test_w8a8_linear_bit_exact(m, n, k, with_bias):
     print(f'[w8a8_linear] m={m} n={n} k={k} bias={with_bias}', flush=True)
@@ -66,6 +67,21 @@ def test_w8a8_linear_bit_exact(m, n, k, with_bias):
     got = host(y)
     assert np.array_equal(got.view(np.uint16), expected.view(np.uint16)), \
         np.argwhere(got.view(np.uint16) != expected.view(np.uint16))[:5]
+
+
+def test_w8a8_linear_prefill_sampled_rows_bit_exact():
+    """configs[2]-sized batch (M = 4096, 5120 -> 5120: 128-row x tiles, four
+    weight tiles per wave), checked bit for bit on 48 sampled rows."""
+    rng = np.random.default_rng(4096)
+    m, n, k = 4096, 5120, 5120
+    qx = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qw = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    xs = (rng.random(m) * 0.05 + 1e-4).astype(np.float32)
+    wsc = (rng.random(n) * 0.002 + 1e-5).astype(np.float32)
+    y = host(_native.w8a8_linear(dev(qx), dev(xs), dev(qw), dev(wsc)))
+    rows = np.sort(rng.choice(m, 48, replace=False))
+    expected = qdq.w8a8_linear_int(qx[rows], xs[rows], qw, wsc)
+    assert np.array_equal(y[rows].view(np.uint16), expected.view(np.uint16))
 
 
 def test_w8a8_linear_rejects_unsupported_k():
