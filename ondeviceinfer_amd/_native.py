@@ -241,20 +241,23 @@ def w8a16_workspace_size(m: int, n: int, k: int) -> int:
 _workspaces: dict = {}
 
 
-def shared_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+def shared_workspace(device: torch.device, nbytes: int, layout: tuple) -> torch.Tensor | None:
     """Zero-filled workspace for callers that do not bring their own.
 
-    One buffer per device, grown on demand and never freed (a graph may have
-    captured its address).  The kernels leave it zeroed after every call, so
-    calls ordered on one stream can share it; concurrent streams need their
-    own workspace (pass ``workspace=``).
+    One buffer per (device, layout), never freed (a graph may have captured
+    its address).  ``layout`` names the operation and the shape that fix where
+    its counters and partials lie (e.g. ``('w4a16', n, k, group)``): the
+    kernels return the counters to zero after every call but leave partials
+    behind, so buffers are shared only between calls with the same layout,
+    and only when those calls are ordered on one stream (concurrent streams
+    need their own workspace: pass ``workspace=``).
     """
     if nbytes <= 0:
         return None
-    key = (device.type, device.index)
+    key = (device.type, device.index) + tuple(layout)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _workspaces.setdefault(('retired',) + key, []).append(_workspaces.get(key))
         _workspaces[key] = buf
     return buf
@@ -275,7 +278,7 @@ def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: in
         if out.data_ptr() % 16:
             raise ValueError('out must be 16-byte aligned')
     if workspace is None and m <= 4:
-        workspace = shared_workspace(device, w4a16_workspace_size(m, n, k, group_size))
+        workspace = shared_workspace(device, w4a16_workspace_size(m, n, k, group_size), ('w4a16', m, n, k, group_size))
     ws_ptr, ws_bytes = None, 0
     if workspace is not None:
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
@@ -313,7 +316,7 @@ def w4a16_decode_fused(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor,
     elif out.dtype != torch.float16 or out.numel() != n or not out.is_contiguous():
         raise ValueError(f'out must be contiguous float16 with {n} elements')
     if workspace is None:
-        workspace = shared_workspace(device, w4a16_workspace_size(1, n, k, group_size))
+        workspace = shared_workspace(device, w4a16_workspace_size(1, n, k, group_size), ('w4a16', 1, n, k, group_size))
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
                                                              workspace.numel() * workspace.element_size())
     _call('wq_w4a16_decode_fused', _ptr(x), k, _ptr(tiles), _ptr(meta), n, group_size, x_mode, _ptr(norm_weight),
@@ -360,7 +363,7 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bi
     else:
         _check(out, torch.float16, (m, n), 'out')
     if workspace is None and m <= 4:
-        workspace = shared_workspace(device, w8a16_workspace_size(m, n, k))
+        workspace = shared_workspace(device, w8a16_workspace_size(m, n, k), ('w8a16', m, n, k))
     ws_ptr, ws_bytes = None, 0
     if workspace is not None:
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
@@ -498,7 +501,7 @@ def decode_attention(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: tor
         _check(out, torch.float16, (q_heads * head_dim,), 'out')
     need = decode_attention_workspace_size(q_heads, kv_heads, head_dim, max_seq)
     if workspace is None and need:
-        workspace = shared_workspace(device, need)
+        workspace = shared_workspace(device, need, ('attention', q_heads, kv_heads, max_seq))
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
                                                              workspace.numel() * workspace.element_size())
     _call('wq_decode_attention', _ptr(qkv), q_heads, kv_heads, head_dim, _ptr(q_norm), _ptr(k_norm), float(eps),

@@ -58,6 +58,23 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v + dpp_f<0x140>(v);
 }
 
+// Lane c's value, wave-uniform.
+__device__ __forceinline__ float lane_f(float v, int c) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c));
+}
+
+// Whole-wave max / sum: the four DPP row results combined from lane reads
+// (the sum in row order).
+__device__ __forceinline__ float wave_max_rl(float v) {
+  v = row_max16(v);
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum_rl(float v) {
+  v = row_sum16(v);
+  return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
+}
+
 // ------------------------------------------------------------------ RMSNorm
 // One workgroup per row, eight elements per thread per step.  out_sum may
 // alias x: each thread rereads only what it wrote itself.
@@ -410,38 +427,32 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
 
 // Merge of the workgroup partials of one query head: grid = q_heads, 128
 // threads (one output element each).  The NC <= NCM partial outputs are
-// requested at once (at chunk indices clamped below NC); meanwhile wave 0
-// turns the chunks' (max, sum) pairs, one per lane, into weights
-// w_c = 2^(m_c - M) (0 for an empty chunk, whose output slot holds zeros)
-// and their weighted sum.  Then out = sum_c w_c O_c / sum_c w_c l_c, summed
-// in chunk order.  With no non-empty chunk (invalid position) the result is
-// 0 / 0 = NaN.
+// requested at once (at chunk indices clamped below NC, which weigh 0).
+// Each wave holds the chunks' (max, sum) pairs one per lane and turns them
+// into weights w_c = 2^(m_c - M) (0 for an empty chunk, whose output slot
+// holds zeros) and sum_c w_c l_c with DPP row reductions and lane reads, so
+// the merge needs no LDS and no barrier; lane c's weight is read out with
+// v_readlane.  out = sum_c w_c O_c / sum_c w_c l_c, summed in chunk order.
+// With no non-empty chunk (invalid position) the result is 0 / 0 = NaN.
 template <int NCM>
 __global__ __launch_bounds__(128) void decode_attention_merge_kernel(int NC, const float* __restrict__ ws_o,
                                                                      const float2_t* __restrict__ ws_ml,
                                                                      half_t* __restrict__ out) {
   constexpr int D = kHeadDim;
-  static_assert(NCM <= kMaxChunks && kMaxChunks <= 64, "wave 0 holds one chunk per lane");
-  __shared__ __attribute__((aligned(16))) float sw[kMaxChunks];
-  __shared__ float sden;
-  const int qh = blockIdx.x, d = threadIdx.x;
+  static_assert(NCM <= kMaxChunks && kMaxChunks <= 64, "one chunk per lane");
+  const int qh = blockIdx.x, d = threadIdx.x, lane = d & 63;
   const float* po = ws_o + (size_t)qh * NC * D + d;
   float part[NCM];
 #pragma unroll
   for (int c = 0; c < NCM; ++c) part[c] = po[(size_t)min(c, NC - 1) * D];
-  if (d < 64) {
-    const float2_t ml = d < NC ? ws_ml[(size_t)qh * NC + d] : float2_t{-INFINITY, 0.f};
-    const float M = wave_max(ml.x);
-    const float w = ml.x == -INFINITY ? 0.f : exp2_hw(ml.x - M);
-    if (d < kMaxChunks) sw[d] = w;
-    const float den = wave_sum(w * ml.y);
-    if (d == 0) sden = den;
-  }
-  __syncthreads();
+  const float2_t ml = lane < NC ? ws_ml[(size_t)qh * NC + lane] : float2_t{-INFINITY, 0.f};
+  const float M = wave_max_rl(ml.x);
+  const float w = ml.x == -INFINITY ? 0.f : exp2_hw(ml.x - M);
+  const float den = wave_sum_rl(w * ml.y);
   float num = 0.f;
 #pragma unroll
-  for (int c = 0; c < NCM; ++c) num += sw[c] * part[c];
-  out[(size_t)qh * D + d] = (half_t)(num / sden);
+  for (int c = 0; c < NCM; ++c) num += lane_f(w, c) * part[c];
+  out[(size_t)qh * D + d] = (half_t)(num / den);
 }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -553,7 +564,10 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
   if (nc > 1) {
     const int rc2 = check_launch("decode_attention");
     if (rc2 != WQ_OK) return rc2;
-    auto merge = nc <= 32 ? decode_attention_merge_kernel<32> : decode_attention_merge_kernel<64>;
+    auto merge = nc <= 16   ? decode_attention_merge_kernel<16>
+                 : nc <= 32 ? decode_attention_merge_kernel<32>
+                 : nc <= 48 ? decode_attention_merge_kernel<48>
+                            : decode_attention_merge_kernel<64>;
     hipLaunchKernelGGL(merge, dim3((unsigned)q_heads), dim3(kHeadDim), 0, as_stream(stream), (int)nc, po,
                        reinterpret_cast<const float2_t*>(ml), reinterpret_cast<half_t*>(out));
     return check_launch("decode_attention_merge");

@@ -203,6 +203,23 @@ def test_w4a16_split_k_workspace_contract(gpu):
     assert torch.count_nonzero(counters).item() == 0      # per-tile counters re-armed
 
 
+def test_default_workspaces_of_different_layouts_do_not_mix(gpu):
+    """Split linears of different tile counts called without a workspace,
+    interleaved: each layout's counters must not land on another's partials."""
+    cases = []
+    for n, seed in ((1024, 21), (5120, 22)):
+        name = 'mlp.down_proj.weight'
+        weights, x = synth.w4_case(n, 17408, 1, seed=seed, name=name)
+        _, layer = prepared_w4(weights, name, gpu)
+        prep = layer['mlp.down_proj._prepared']
+        assert _native.w4a16_workspace_size(1, n, 17408, 128) > 0
+        cases.append((n, prep, dev(x, gpu), qdq.qdq_linear(x, weights, name)))
+    for rep in range(2):
+        for n, prep, xd, expected in cases:
+            got = host(_native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128))
+            check_parity(got, expected, f'default workspace n={n} call {rep}')
+
+
 def test_w4a16_graph_replays_match_eager(gpu):
     """HIP-graph capture of decode GEMVs (split and unsplit shapes), replayed
     several times with eager work in between; every replay equals eager."""
