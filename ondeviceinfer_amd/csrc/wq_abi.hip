@@ -107,8 +107,9 @@ extern "C" int wq_w4a16_decode_fused(const uint16_t* x, int64_t k, const void* t
   WQ_REQUIRE(x_mode != 1 || (norm_weight && sumsq_in && sumsq_count > 0 && sumsq_count <= 512),
              WQ_ERR_INVALID_ARGUMENT, "rmsnorm mode needs norm_weight, sumsq_in and 0 < sumsq_count <= 512");
   WQ_REQUIRE(aligned16(x) && aligned16(tiles) && aligned16(y) && (reinterpret_cast<uintptr_t>(meta) & 7u) == 0 &&
-                 aligned16(norm_weight) && (reinterpret_cast<uintptr_t>(residual) & 7u) == 0,
-             WQ_ERR_INVALID_ARGUMENT, "x, tiles, y and norm_weight must be 16-byte aligned, meta and residual 8-byte");
+                 aligned16(norm_weight) && aligned16(sumsq_in) && (reinterpret_cast<uintptr_t>(residual) & 7u) == 0,
+             WQ_ERR_INVALID_ARGUMENT,
+             "x, tiles, y, norm_weight and sumsq_in must be 16-byte aligned, meta and residual 8-byte");
   return launch_w4_gemv_fused(reinterpret_cast<const half_t*>(x), (int)k, reinterpret_cast<const uint4_t*>(tiles),
                               reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, x_mode,
                               reinterpret_cast<const half_t*>(norm_weight), sumsq_in, (int)sumsq_count, eps,

@@ -187,6 +187,44 @@ __device__ __forceinline__ half8_t ld_h8(const half_t* p) {
   return *reinterpret_cast<const half8_t*>(p);
 }
 
+// Cross-lane reductions without LDS: DPP moves inside the 16-lane rows, then
+// v_readlane for the wave (every lane gets the result; sums in row order).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Over the 16 lanes of a DPP row: quad swaps, then the half-row and row
+// mirrors.
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_f<0xb1>(v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4e>(v));    // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+  return fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_f<0xb1>(v);
+  v += dpp_f<0x4e>(v);
+  v += dpp_f<0x141>(v);
+  return v + dpp_f<0x140>(v);
+}
+
+// Lane c's value, wave-uniform.
+__device__ __forceinline__ float lane_f(float v, int c) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c));
+}
+
+__device__ __forceinline__ float wave_max_rl(float v) {
+  v = row_max16(v);
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum_rl(float v) {
+  v = row_sum16(v);
+  return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // 2^x on the transcendental unit (v_exp_f32, about 1 ulp; -inf -> 0).

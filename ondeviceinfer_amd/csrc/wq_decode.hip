@@ -25,55 +25,6 @@ constexpr int kMaxChunks = 64;    // attention workgroups per kv head (one merge
 constexpr int kMaxSpc = 4;        // sub-chunks per workgroup
 constexpr int kMaxSeq = kMaxChunks * kMaxSpc * kSub;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-
-// Reductions over the 16 lanes of a DPP row (every lane gets the result):
-// quad swaps, then the half-row and row mirrors.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float row_max16(float v) {
-  v = fmaxf(v, dpp_f<0xb1>(v));    // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_f<0x4e>(v));    // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
-  return fmaxf(v, dpp_f<0x140>(v));  // row_mirror
-}
-
-__device__ __forceinline__ float row_sum16(float v) {
-  v += dpp_f<0xb1>(v);
-  v += dpp_f<0x4e>(v);
-  v += dpp_f<0x141>(v);
-  return v + dpp_f<0x140>(v);
-}
-
-// Lane c's value, wave-uniform.
-__device__ __forceinline__ float lane_f(float v, int c) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c));
-}
-
-// Whole-wave max / sum: the four DPP row results combined from lane reads
-// (the sum in row order).
-__device__ __forceinline__ float wave_max_rl(float v) {
-  v = row_max16(v);
-  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
-}
-
-__device__ __forceinline__ float wave_sum_rl(float v) {
-  v = row_sum16(v);
-  return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
-}
 
 // ------------------------------------------------------------------ RMSNorm
 // One workgroup per row, eight elements per thread per step.  out_sum may
@@ -95,7 +46,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const half_t* x, const
       ss += f * f;
     }
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_rl(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float r = rsqrtf((part[0] + part[1] + part[2] + part[3]) / (float)n + eps);
@@ -143,7 +94,7 @@ __device__ __forceinline__ half2_t norm_rope_pair(half2_t v, bool norm, half2_t 
 #pragma clang fp contract(off)
   if (norm) {
     const float a = (float)v[0], b = (float)v[1];
-    const float r = rsqrtf(wave_sum(a * a + b * b) * (1.0f / kHeadDim) + eps);
+    const float r = rsqrtf(wave_sum_rl(a * a + b * b) * (1.0f / kHeadDim) + eps);
     v[0] = nw[0] * (half_t)(a * r);
     v[1] = nw[1] * (half_t)(b * r);
   }

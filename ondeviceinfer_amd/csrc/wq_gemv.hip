@@ -309,12 +309,6 @@ struct FuseArgs {
   float* sumsq_out;        // per-16-row tile sum of squares of y (for the next RmsNorm)
 };
 
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 // Eight x values -> w * fp16(x * r), the reference's rms_norm order
 // (normalize in fp32, cast, scale in fp16).
 __device__ __forceinline__ uint4_t rms_scale8(uint4_t xv, uint4_t wv, float r) {
@@ -374,8 +368,11 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
   //    loads below are in flight.
   uint4_t xr[kXPerLane];
   uint4_t xa[XM == XMode::Plain ? 1 : kXPerLane];   // up half (SiluMul) or norm weight (RmsNorm)
-  constexpr int kSqPerLane = 8;                     // sums of squares held per lane before the weights
-  float sq[XM == XMode::RmsNorm ? kSqPerLane : 1];
+  // The producer's sums of squares (<= 512): 16-byte loads of the first
+  // count & ~3 (two per lane) and one load of the remainder.
+  constexpr int kSqPerLane = 2;
+  float4_t sq[XM == XMode::RmsNorm ? kSqPerLane : 1];
+  float sqt = 0.f;
   auto x_offset = [&](int j) { return min(b0 * kW4BlockK + (min(lane + 64 * j, kXChunks - 1) % (NBX * 16)) * 8, K - 8); };
 #pragma unroll
   for (int j = 0; j < kXPerLane; ++j) {
@@ -388,7 +385,9 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
   if constexpr (XM == XMode::RmsNorm) {
     // Unconditional (clamped) loads; entries past the count are dropped when summed.
 #pragma unroll
-    for (int u = 0; u < kSqPerLane; ++u) sq[u] = fz.sumsq_in[min(lane + 64 * u, fz.sumsq_count - 1)];
+    for (int u = 0; u < kSqPerLane; ++u)
+      sq[u] = reinterpret_cast<const float4_t*>(fz.sumsq_in)[max(min(lane + 64 * u, fz.sumsq_count / 4 - 1), 0)];
+    sqt = fz.sumsq_in[min((fz.sumsq_count & ~3) + (lane & 3), fz.sumsq_count - 1)];
   }
   // The fused residual (W4, M = 1; wave 0 stores the tile) is fetched now so
   // that its latency is not added after the reduction (for NB <= 8, where the
@@ -446,8 +445,10 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
   if constexpr (XM == XMode::RmsNorm) {
     float ss = 0.f;
 #pragma unroll
-    for (int u = 0; u < kSqPerLane; ++u) ss += lane + 64 * u < fz.sumsq_count ? sq[u] : 0.f;
-    const float r = rsqrtf(wave_sum_f(ss) / (float)K + fz.eps);
+    for (int u = 0; u < kSqPerLane; ++u)
+      ss += lane + 64 * u < fz.sumsq_count / 4 ? (sq[u][0] + sq[u][1]) + (sq[u][2] + sq[u][3]) : 0.f;
+    ss += lane < (fz.sumsq_count & 3) ? sqt : 0.f;
+    const float r = rsqrtf(wave_sum_rl(ss) / (float)K + fz.eps);
 #pragma unroll
     for (int j = 0; j < kXPerLane; ++j) xr[j] = rms_scale8(xr[j], xa[j], r);
   }
@@ -550,8 +551,7 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ?
 #pragma unroll
           for (int v = 0; v < 4; ++v) q += (float)o[v] * (float)o[v];
         }
-        q += __shfl_xor(q, 16);
-        q += __shfl_xor(q, 32);
+        q = (lane_f(q, 0) + lane_f(q, 16)) + (lane_f(q, 32) + lane_f(q, 48));
         if (lane == 0) fz.sumsq_out[tile] = q;
       }
     } else {
