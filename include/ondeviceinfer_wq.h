@@ -108,7 +108,8 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
  *   x_mode 0  x as given ([k]);
  *   x_mode 1  x <- norm_weight * fp16(x * rsqrt(sum(sumsq_in[0..sumsq_count)) / k + eps)),
  *             the RMSNorm of x whose sum of squares the producing linear
- *             left in sumsq_in (one float per 16-row tile, at most 512);
+ *             left in sumsq_in (one float per 16-row tile, at most 512;
+ *             16-byte aligned);
  *   x_mode 2  x is [gate | up] of length 2k and x <- fp16(fp16(silu(gate)) * up);
  *   residual  if not NULL, y = residual + fp16(x . W^T) (fp16 add; may alias y);
  *   sumsq_out if not NULL, receives the sum of squares of y per 16-row tile
