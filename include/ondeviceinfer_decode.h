@@ -61,6 +61,23 @@ int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t kv_heads, 
                         uint16_t* key_cache, uint16_t* value_cache, int64_t max_seq, float scale, uint16_t* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes for wq_lm_head with token != NULL (the per-wave argmax
+ * candidates; no initialization needed). */
+int wq_lm_head_workspace_size(int64_t k, int64_t vocab, size_t* bytes);
+
+/* The fp16 LM head of one decode token and its greedy token:
+ *   logits[v] = fp16(sum_k weight[v, k] * x[k])  (fp32 accumulation), and
+ *   *token    = the first v with the largest logits[v] (NaN counts as the
+ *               largest value), i.e. torch.argmax over the fp16 logits.
+ * weight is the row-major fp16 [vocab, k] LM-head matrix, k % 512 == 0 and
+ * k <= 8192; logits (fp16 [vocab]) or token (one int64) may be NULL, not
+ * both.  x and weight 16-byte aligned.
+ * Replaces: `F.linear(hidden_states, self.lm_head)` (quantized_model.py:337)
+ * and `output.logits[:, -1].argmax(dim=-1, keepdim=True)` (generation.py:47,
+ * :58) for one token. */
+int wq_lm_head(const uint16_t* x, int64_t k, const uint16_t* weight, int64_t vocab, uint16_t* logits,
+               int64_t* token, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

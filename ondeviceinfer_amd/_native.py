@@ -62,6 +62,8 @@ _SIGNATURES = {
     'wq_decode_attention_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
     'wq_decode_attention': [_P, _I64, _I64, _I64, _P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _I64,
                             ctypes.c_float, _P, _P, ctypes.c_size_t, _P],
+    'wq_lm_head_workspace_size': [_I64, _I64, _SIZE_P],
+    'wq_lm_head': [_P, _I64, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
 }
 EXPORTED_SYMBOLS = ('wq_last_error', *_SIGNATURES)
 
@@ -508,3 +510,39 @@ def decode_attention(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: tor
           _ptr(cos_table), _ptr(sin_table), _ptr(position), _ptr(key_cache), _ptr(value_cache), max_seq,
           float(scale), _ptr(out), ws_ptr, ws_bytes, _stream(device))
     return out
+
+
+def lm_head_workspace_size(k: int, vocab: int) -> int:
+    b = ctypes.c_size_t()
+    _call('wq_lm_head_workspace_size', k, vocab, ctypes.byref(b))
+    return b.value
+
+
+def lm_head(x: torch.Tensor, weight: torch.Tensor, *, logits: torch.Tensor | None = None,
+            token: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+            want_logits: bool = True, want_token: bool = True) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """fp16 LM head of one token (``x`` [k], ``weight`` [vocab, k]) and its
+    greedy token (``torch.argmax`` over the fp16 logits) in one pass:
+    ``wq_lm_head``.  Returns ``(logits [vocab] fp16, token [1] int64)``."""
+    device = _require_gpu(x, weight, logits, token, workspace)
+    if weight.dim() != 2:
+        raise ValueError(f'weight must be [vocab, k], got {tuple(weight.shape)}')
+    vocab, k = weight.shape
+    _check(weight, torch.float16, (vocab, k), 'weight')
+    if x.dtype != torch.float16 or not x.is_contiguous() or x.numel() != k:
+        raise ValueError(f'x must be contiguous float16 with {k} elements')
+    if logits is None and want_logits:
+        logits = torch.empty(vocab, dtype=torch.float16, device=device)
+    if logits is not None:
+        _check(logits.view(-1), torch.float16, (vocab,), 'logits')
+    if token is None and want_token:
+        token = torch.empty(1, dtype=torch.int64, device=device)
+    if token is not None and (token.dtype != torch.int64 or token.numel() != 1 or not token.is_contiguous()):
+        raise ValueError('token must be one contiguous int64')
+    if workspace is None and token is not None:
+        workspace = shared_workspace(device, lm_head_workspace_size(k, vocab), ('lm_head', k, vocab))
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                             workspace.numel() * workspace.element_size())
+    _call('wq_lm_head', _ptr(_aligned(x)), k, _ptr(weight), vocab, _ptr(logits), _ptr(token), ws_ptr, ws_bytes,
+          _stream(device))
+    return logits, token

@@ -4,7 +4,7 @@ Same call sequence and timing boundaries as the reference: one prefill call
 with ``logits_to_keep=1``, then one model call per generated token, with
 ``torch.cuda.synchronize`` around each phase.  On this build each single-token
 call of ``QuantizedQwen3ForCausalLM`` replays a captured HIP graph of the
-whole decode step.
+whole decode step, whose LM head also returns the greedy token.
 """
 from __future__ import annotations
 
@@ -28,6 +28,14 @@ class GenerationResult:
         return decode_tokens / self.decode_seconds if self.decode_seconds > 0 else 0.0
 
 
+def _greedy(output) -> Tensor:
+    """``output.logits[:, -1].argmax(dim=-1, keepdim=True)``; a decode-graph
+    step already picked it with the LM head (same rule: the first index of the
+    largest fp16 logit) and hands it over as ``next_token``."""
+    token = getattr(output, 'next_token', None)
+    return token if token is not None else output.logits[:, -1].argmax(dim=-1, keepdim=True)
+
+
 @torch.inference_mode()
 def greedy_generate(model, input_ids: Tensor, *, max_new_tokens: int, cache, eos_token_id: int | None = None
                     ) -> GenerationResult:
@@ -40,7 +48,7 @@ def greedy_generate(model, input_ids: Tensor, *, max_new_tokens: int, cache, eos
         torch.cuda.synchronize(device)
     start = time.perf_counter()
     output = model(input_ids, cache=cache, logits_to_keep=1)
-    next_token = output.logits[:, -1].argmax(dim=-1, keepdim=True)
+    next_token = _greedy(output)
     if device.type == 'cuda':
         torch.cuda.synchronize(device)
     prefill_seconds = time.perf_counter() - start
@@ -51,7 +59,7 @@ def greedy_generate(model, input_ids: Tensor, *, max_new_tokens: int, cache, eos
         if eos_token_id is not None and bool(torch.all(next_token == eos_token_id)):
             break
         output = model(next_token, cache=cache, logits_to_keep=1)
-        next_token = output.logits[:, -1].argmax(dim=-1, keepdim=True)
+        next_token = _greedy(output)
         generated.append(next_token)
     if device.type == 'cuda':
         torch.cuda.synchronize(device)

@@ -104,6 +104,9 @@ GATE_UP_FUSED = 'mlp.gate_up_proj.weight'
 class CausalLMOutput:
     logits: Tensor
     cache: object | None = None
+    # Greedy token of the last position ([batch, 1] int64), when the decode
+    # graph computed it with the LM head (torch.argmax over the fp16 logits).
+    next_token: Tensor | None = None
 
 
 def _has_prepared(weights: Mapping, name: str) -> bool:
@@ -169,10 +172,12 @@ class DecodeStepGraph:
     linear (RMSNorm in its prologue), attention (q/k norm, RoPE, KV append,
     GQA softmax, chunk merge), o linear (+ residual), fused gate_up linear
     (RMSNorm prologue), down linear (SiLU*up prologue, + residual)] -> final
-    norm -> fp16 LM head.  W8 weights take the same steps with the norms,
-    residual adds and SiLU*up as separate kernels.  Inputs are the token id
-    and the position (device scalars); every launch is a HIP kernel of this
-    library except the embedding gather and the fp16 LM-head GEMM (torch)."""
+    norm -> fp16 LM head with the greedy token picked in the same pass.  W8
+    weights take the same steps with the norms, residual adds and SiLU*up as
+    separate kernels.  Inputs are the token id and the position (device
+    scalars); every launch is a HIP kernel of this library except the
+    embedding gather (torch), and the LM head falls back to torch's GEMM
+    when the hidden size is not a multiple of 512."""
 
     def __init__(self, model: 'QuantizedQwen3ForCausalLM', key_cache: list[Tensor], value_cache: list[Tensor],
                  max_seq_len: int):
@@ -195,6 +200,10 @@ class DecodeStepGraph:
         self.gate_up = torch.empty(1, 2 * cfg.intermediate_size, **f16)
         self.act = torch.empty(1, cfg.intermediate_size, **f16)
         self.logits = torch.empty(1, cfg.vocab_size, **f16)
+        self.next_token = torch.zeros(1, dtype=torch.long, device=dev)
+        self.native_lm_head = hidden % 512 == 0 and hidden <= 8192 and model.lm_head.is_contiguous()
+        self.lm_ws = torch.zeros(max(_native.lm_head_workspace_size(hidden, cfg.vocab_size), 1), dtype=torch.uint8,
+                                 device=dev) if self.native_lm_head else None
         self.attn_ws = torch.zeros(max(_native.decode_attention_workspace_size(hq, hkv, d, max_seq_len), 1),
                                    dtype=torch.uint8, device=dev)
         self.scale = 1.0 / float(d) ** 0.5
@@ -265,7 +274,15 @@ class DecodeStepGraph:
                                    x_mode=nat.X_SILU_MUL, residual=hid, sumsq_out=self.sumsq_down, out=hid,
                                    workspace=dn_p.workspace)
         nat.add_rmsnorm(self.hidden, self.model.final_norm, eps, out=self.states)
-        torch.mm(self.states, self.lm_head_t, out=self.logits)
+        self._lm_head()
+
+    def _lm_head(self) -> None:
+        if self.native_lm_head:
+            _native.lm_head(self.states.view(-1), self.model.lm_head, logits=self.logits.view(-1),
+                            token=self.next_token, workspace=self.lm_ws)
+        else:
+            torch.mm(self.states, self.lm_head_t, out=self.logits)
+            torch.argmax(self.logits.view(-1), out=self.next_token.view(()))
 
     def _step_unfused(self) -> None:
         cfg = self.model.config
@@ -286,7 +303,7 @@ class DecodeStepGraph:
             _native.silu_mul(self.gate_up, out=self.act)
             self._linear(self.act, w, 'mlp.down_proj.weight', self.delta)
         _native.add_rmsnorm(self.hidden, self.model.final_norm, eps, delta=self.delta, out=self.states)
-        torch.mm(self.states, self.lm_head_t, out=self.logits)
+        self._lm_head()
 
     def run(self, token: Tensor, position: int) -> Tensor:
         if not 0 <= position < self.max_seq_len:
@@ -374,7 +391,8 @@ class QuantizedQwen3ForCausalLM:
                 raise RuntimeError('decode graph needs every layer of the cache at the same length')
             logits = graph.run(input_ids.to(self.device), past)
             cache.lengths[:] = [past + 1] * len(cache.lengths)
-            return CausalLMOutput(logits=logits.view(1, 1, -1).clone(), cache=cache)
+            return CausalLMOutput(logits=logits.view(1, 1, -1).clone(), cache=cache,
+                                  next_token=graph.next_token.view(1, 1).clone())
 
         ids_cpu = input_ids.detach().to(device='cpu')
         hidden_cpu = F.embedding(ids_cpu, self.store.embed_tokens)

@@ -237,3 +237,68 @@ def test_w4a16_decode_fused_matches_oracle(nat, k, n, mode):
     assert qdq.parity_ok(m), m
     g64 = got.astype(np.float64)
     assert np.allclose(ss.cpu().numpy(), (g64 ** 2).reshape(-1, 16).sum(-1), rtol=1e-5, atol=1e-3)
+
+
+# ------------------------------------------------------------------ LM head + greedy token
+
+def _lm_case(vocab, k, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(k) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((vocab, k)) * 0.05).astype(np.float16)
+    return x, w
+
+
+@pytest.mark.parametrize('vocab,k', [(1, 512), (3, 1024), (1000, 512), (4097, 4096), (20000, 8192),
+                                     (151936, 5120)])
+def test_lm_head_logits_and_token(nat, vocab, k):
+    """fp16 logits against the fp32-accumulated oracle; the token is exactly
+    torch.argmax of the returned logits (first index of the largest)."""
+    print(f'[lm_head] vocab={vocab} k={k}', flush=True)
+    x, w = _lm_case(vocab, k, seed=vocab + k)
+    tx, tw = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    logits, token = nat.lm_head(tx, tw)
+    torch.cuda.synchronize()
+    ref = qdq.linear_fp32(x[None], w)[0]
+    m = qdq.parity_metrics(logits.cpu().numpy(), ref)
+    assert qdq.parity_ok(m), m
+    assert token.item() == int(torch.argmax(logits).item())
+    # Where the oracle's top two are apart by more than the fp16 step, the
+    # token is the oracle's too.
+    if vocab > 1:
+        top2 = np.sort(ref.astype(np.float32))[-2:]
+        if top2[1] - top2[0] > 4e-3 * max(abs(top2[1]), 1.0):
+            assert token.item() == int(np.argmax(ref))
+
+
+def test_lm_head_ties_nan_and_infinities(nat):
+    k, vocab = 512, 3000
+    x = np.ones(k, dtype=np.float16)
+    w = np.zeros((vocab, k), dtype=np.float16)
+    w[17, :] = 0.01
+    w[2500, :] = 0.01           # same logit as row 17: the first index wins
+    tx = torch.from_numpy(x).cuda()
+    _, token = nat.lm_head(tx, torch.from_numpy(w).cuda())
+    assert token.item() == 17
+    w[1200, 0] = np.nan         # a NaN logit counts as the largest (torch.argmax)
+    w[2900, 0] = np.nan
+    logits, token = nat.lm_head(tx, torch.from_numpy(w).cuda())
+    assert token.item() == 1200 == int(torch.argmax(logits).item())
+    w = np.full((vocab, k), -60000, dtype=np.float16)   # every logit overflows to -inf
+    logits, token = nat.lm_head(tx, torch.from_numpy(w).cuda())
+    assert torch.isneginf(logits).all() and token.item() == 0
+
+
+def test_lm_head_only_logits_or_only_token(nat):
+    x, w = _lm_case(5000, 1024, seed=5)
+    tx, tw = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    both_l, both_t = nat.lm_head(tx, tw)
+    only_l, none_t = nat.lm_head(tx, tw, want_token=False)
+    none_l, only_t = nat.lm_head(tx, tw, want_logits=False)
+    torch.cuda.synchronize()
+    assert none_t is None and none_l is None
+    assert torch.equal(both_l, only_l) and torch.equal(both_t, only_t)
+    with pytest.raises(ValueError, match='k % 512'):
+        nat.lm_head(torch.zeros(640, dtype=torch.float16, device='cuda'),
+                    torch.zeros(8, 640, dtype=torch.float16, device='cuda'))
+    with pytest.raises(ValueError, match='workspace'):
+        nat.lm_head(tx, tw, workspace=torch.zeros(8, dtype=torch.uint8, device='cuda'))
