@@ -10,7 +10,7 @@ is one decode token: a replay of the captured decode-step graph (40 x [QKV
 GEMV with the input RMSNorm in its prologue, attention (q/k norm, RoPE, cache
 append, GQA) + chunk merge, o GEMV + residual, gate_up GEMV with the
 post-attention RMSNorm in its prologue, down GEMV with SiLU*up in its prologue
-+ residual], final norm, fp16 LM head) plus the argmax.
++ residual], final norm, fp16 LM head with the greedy token).
 After the prefill and ``--warmup`` untimed steps, ``--steps`` steps are timed;
 ``value`` = steps / seconds (tok/s), compared with the reference's published
 26.358 tok/s (AWQ-INT4 + Marlin, RTX 3090, same workload).
@@ -187,6 +187,7 @@ def main() -> int:
 
     import torch
     from ondeviceinfer_amd import _native as native
+    from ondeviceinfer_amd.generation import greedy_token
 
     if not torch.cuda.is_available():
         print('bench.py needs a GPU', file=sys.stderr)
@@ -206,15 +207,15 @@ def main() -> int:
         torch.cuda.synchronize()
         t_p = time.perf_counter()
         out = model(prompt, cache=cache, logits_to_keep=1)
-        token = out.logits[:, -1].argmax(dim=-1, keepdim=True)
+        token = greedy_token(out)
         torch.cuda.synchronize()
         prefill_s = time.perf_counter() - t_p
         for _ in range(n_untimed):
-            token = model(token, cache=cache, logits_to_keep=1).logits[:, -1].argmax(dim=-1, keepdim=True)
+            token = greedy_token(model(token, cache=cache, logits_to_keep=1))
         torch.cuda.synchronize()
         t_d = time.perf_counter()
         for _ in range(n_timed):
-            token = model(token, cache=cache, logits_to_keep=1).logits[:, -1].argmax(dim=-1, keepdim=True)
+            token = greedy_token(model(token, cache=cache, logits_to_keep=1))
         torch.cuda.synchronize()
         return prefill_s, time.perf_counter() - t_d, cache
 
@@ -238,7 +239,7 @@ def main() -> int:
         'dtype': 'fp16', 'data': 'synthetic',
         'config': {'workload': f'configs[4]: Qwen3-14B-shaped AWQ-INT4 G=128 decoder ({args.layers} layers), random '
                                f'weights, B=1, {PROMPT}-token random prompt, greedy decode, fp16 KV resident; '
-                               'one step = one decode token (graph replay + argmax)',
+                               'one step = one decode token (graph replay; the LM head picks the greedy token)',
                    'layers': args.layers, 'prompt_tokens': PROMPT, 'group_size': GROUP,
                    'kv_capacity': capacity},
         'prefill_seconds': round(prefill_s, 4),
@@ -368,6 +369,23 @@ def main() -> int:
                         'frac': round(att_bytes / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': True,
                         'launches_per_token': args.layers})
         del g, kc
+        # The fp16 LM head with the greedy token (once per token).
+        lm_x = torch.randn(HIDDEN, device=device).half()
+        lm_logits = torch.empty(cfg.vocab_size, device=device).half()
+        lm_tok = torch.zeros(1, dtype=torch.long, device=device)
+        lm_ws = torch.zeros(native.lm_head_workspace_size(HIDDEN, cfg.vocab_size), dtype=torch.uint8, device=device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(4):
+                native.lm_head(lm_x, model.lm_head, logits=lm_logits, token=lm_tok, workspace=lm_ws)
+        per = time_graph(torch, g, 5) / 4
+        lm_b = cfg.vocab_size * HIDDEN * 2 + HIDDEN * 2 + cfg.vocab_size * 2
+        kernels.append({'op': 'lm_head', 'fusion': 'fp16 GEMV + greedy token (pick launch)',
+                        'shape': f'{HIDDEN}->{cfg.vocab_size}', 'kernel': 'lm_head_kernel<10> + lm_head_pick_kernel',
+                        'bytes': lm_b, 'us_per_launch': round(per * 1e6, 3), 'gbs': round(lm_b / per / 1e9, 1),
+                        'frac': round(lm_b / per / 1e9 / HBM_PEAK_GBS, 4), 'in_decode_step': True,
+                        'launches_per_token': 1})
+        del g
         for e in kernels:
             e['us_per_token'] = round(e['us_per_launch'] * e['launches_per_token'], 2)
         step = [e for e in kernels if e['in_decode_step']]

@@ -28,7 +28,7 @@ class GenerationResult:
         return decode_tokens / self.decode_seconds if self.decode_seconds > 0 else 0.0
 
 
-def _greedy(output) -> Tensor:
+def greedy_token(output) -> Tensor:
     """``output.logits[:, -1].argmax(dim=-1, keepdim=True)``; a decode-graph
     step already picked it with the LM head (same rule: the first index of the
     largest fp16 logit) and hands it over as ``next_token``."""
@@ -48,7 +48,7 @@ def greedy_generate(model, input_ids: Tensor, *, max_new_tokens: int, cache, eos
         torch.cuda.synchronize(device)
     start = time.perf_counter()
     output = model(input_ids, cache=cache, logits_to_keep=1)
-    next_token = _greedy(output)
+    next_token = greedy_token(output)
     if device.type == 'cuda':
         torch.cuda.synchronize(device)
     prefill_seconds = time.perf_counter() - start
@@ -59,7 +59,7 @@ def greedy_generate(model, input_ids: Tensor, *, max_new_tokens: int, cache, eos
         if eos_token_id is not None and bool(torch.all(next_token == eos_token_id)):
             break
         output = model(next_token, cache=cache, logits_to_keep=1)
-        next_token = _greedy(output)
+        next_token = greedy_token(output)
         generated.append(next_token)
     if device.type == 'cuda':
         torch.cuda.synchronize(device)
