@@ -3,13 +3,17 @@
 // Workgroup = 4 waves.  Each wave owns NT 16-row weight tiles (a 16*NT slice
 // of N, disjoint between waves, so no weight is dequantized twice in a
 // workgroup); all four waves share a BM = 16*MT slice of M.  Per 128-k block:
-//  * the activation tile x[BM, 128] is copied global -> LDS with
-//    global_load_lds_dwordx4 (no register staging) into a two-stage ring;
+//  * the activation tile x[BM, 128] is copied buffer -> LDS with
+//    buffer_load_dwordx4 ... lds (no register staging) into a two-stage ring;
 //    16-byte chunk c of row r sits at slot c ^ (r & 15), so the sixteen rows
 //    a B-fragment read touches fall in sixteen different bank groups;
 //  * each wave loads its weight tiles straight from HBM into registers one
 //    block ahead (the W4 tile layout already is the MFMA A-fragment order)
-//    and dequantizes them there;
+//    and dequantizes them there, one tile at a time;
+// Every load goes through a buffer resource with a wave-uniform base and a
+// 32-bit lane offset, so no 64-bit per-lane address stays live and the
+// accumulators fit without spills; rows past M and tiles past N fall
+// outside the buffers and read as zero.
 //  * NT x MT x 4 MFMA v_mfma_f32_16x16x32_f16 accumulate in fp32.
 // W4 weights are dequantized with their group scale, fp16((q - z) * s): the
 // oracle's fp16 weight bit for bit.  INT8 weights enter as exact fp16 q and
@@ -37,15 +41,46 @@ struct WRegs<GFmt::W8, NT> {
   uint4_t a[NT], b[NT];
 };
 
-// 16 bytes per lane global -> LDS (global_load_lds_dwordx4): lane L's bytes
-// land at lds_base + 16 * L.  Kept out of the kernel template: with the
-// builtin written inside it, the host pass drops the kernel's launch stub.
-__device__ __forceinline__ void lds_load16(const void* src, uint8_t* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane L's
+// bytes land at lds_base + 16 * L; offsets at or past the buffer's record
+// count read as zero.  Kept out of the kernel template: with the builtin
+// written inside it, the host pass drops the kernel's launch stub.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0, 0);
 }
+
+// Buffer over [base, base + bytes) (bytes clamped to the 31-bit record count).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int64_t bytes) {
+  const int nrec = (int)(bytes < 0 ? 0 : bytes > 0x7fffffff ? 0x7fffffff : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrec, kBufferRsrcWord3);
+}
+
+constexpr int kNtPolicy = 2;   // non-temporal (streamed once)
 
 // LDS slot (16-byte chunk index inside a 256-byte row) of chunk c in row r.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 15); }
+
+// 16-byte LDS read issued as inline asm.  The compiler cannot tell the
+// buffer -> LDS copies of the next stage from reads of the current one, and
+// before any LDS read it can see it waits for every one of them (vmcnt(0)),
+// which serializes the copy with the math.  These reads are invisible to
+// it, so lds_wait_all() below must complete them before use.
+__device__ __forceinline__ half8_t lds_read16(const uint8_t* p) {
+  const uint32_t a = (uint32_t)(size_t)((const __attribute__((address_space(3))) uint8_t*)p);
+  half8_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+
+// Waits for the first four of eight fragment reads (lgkmcnt(4): LDS reads
+// return in order) or for all of them, tied to the fragments it completes so
+// that no use moves above it.
+__device__ __forceinline__ void lds_wait_first4(half8_t (&b)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+}
+__device__ __forceinline__ void lds_wait_last4(half8_t (&b)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]));
+}
 
 template <GFmt F, int NT, int MT>
 __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restrict__ x, int M, int K,
@@ -65,45 +100,58 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
   const int m0 = blockIdx.y * BM;
   const int tile0 = ((int)blockIdx.x * 4 + wave) * NT;
 
-  int tile[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) tile[t] = min(tile0 + t, ntile - 1);
-
   // Activation copy for block `blk` into stage `st`: instruction J of the
   // workgroup fills rows 4J..4J+3; lane L lands in row 4J + L/16, slot L%16,
-  // so it fetches chunk (L%16) ^ (row & 15) of that row.
+  // so it fetches chunk (L%16) ^ (row & 15) of that row.  The buffer ends at
+  // row M, so rows past it land as zeros.  With kInstrPerWave a multiple of
+  // 4, row & 15 depends only on j & 3 and the lane: four lane offsets.
+  static_assert(kInstrPerWave % 4 == 0, "x copy layout");
+  uint32_t xvo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rl = 4 * q + (lane >> 4);   // row & 15 of instruction j with j & 3 == q
+    xvo[q] = (uint32_t)((lane >> 4) * K * 2 + swz(rl, lane & 15) * 16);
+  }
+  const half_t* xw = x + (size_t)m0 * K;
+  const int64_t x_bytes = (int64_t)(M - m0) * K * 2;
   auto copy_x = [&](int blk, int st) {
+    const __amdgpu_buffer_rsrc_t r = buf_rsrc(xw + (size_t)blk * kW4BlockK, x_bytes - (int64_t)blk * kRowBytes);
 #pragma unroll
     for (int j = 0; j < kInstrPerWave; ++j) {
       const int J = wave * kInstrPerWave + j;
-      const int r = 4 * J + (lane >> 4);
-      const int c = swz(r, lane & 15);
-      const int row = min(m0 + r, M - 1);
-      const half_t* src = x + (size_t)row * K + (size_t)blk * kW4BlockK + c * 8;
-      lds_load16(src, xs + st * kStageBytes + J * 1024);
+      lds_load16(r, xvo[j & 3], (uint32_t)(4 * J * K * 2), xs + st * kStageBytes + J * 1024);
     }
   };
 
+  // This wave's NT weight tiles from tile0 on; tiles past the last read as zero.
+  __amdgpu_buffer_rsrc_t rw, rm;
+  if constexpr (F == GFmt::W4) {
+    const int ngrp = nblk / bpg;
+    rw = buf_rsrc(reinterpret_cast<const uint8_t*>(wsrc) + (size_t)tile0 * nblk * 1024,
+                  (int64_t)(ntile - tile0) * nblk * 1024);
+    rm = buf_rsrc(reinterpret_cast<const uint8_t*>(wmeta) + (size_t)tile0 * ngrp * kW4MetaBytes,
+                  (int64_t)(ntile - tile0) * ngrp * kW4MetaBytes);
+  } else {
+    rw = buf_rsrc(reinterpret_cast<const int8_t*>(wsrc) + (size_t)tile0 * 16 * K, (int64_t)(N - tile0 * 16) * K);
+  }
   auto fetch_w = [&](int blk, WRegs<F, NT>& r) {
     if constexpr (F == GFmt::W4) {
-      const uint4_t* tiles = reinterpret_cast<const uint4_t*>(wsrc);
-      const uint8_t* meta = reinterpret_cast<const uint8_t*>(wmeta);
       const int ngrp = nblk / bpg, g = blk / bpg;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        r.w[t] = __builtin_nontemporal_load(tiles + ((size_t)tile[t] * nblk + blk) * 64 + lane);
-        const uint8_t* mp = meta + ((size_t)tile[t] * ngrp + g) * kW4MetaBytes;
-        r.s[t] = reinterpret_cast<const uint16_t*>(mp)[i];
-        r.z[t] = reinterpret_cast<const uint32_t*>(mp + 32)[i >> 3];
+        r.w[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)lane * 16, (uint32_t)((t * nblk + blk) * 1024),
+                                                       kNtPolicy);
+        const uint32_t mo = (uint32_t)((t * ngrp + g) * kW4MetaBytes);
+        r.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rm, (uint32_t)i * 2, mo, 0);
+        r.z[t] = __builtin_amdgcn_raw_buffer_load_b32(rm, 32 + (uint32_t)(i >> 3) * 4, mo, 0);
       }
     } else {
-      const int8_t* q = reinterpret_cast<const int8_t*>(wsrc);
+      const uint32_t vo = (uint32_t)(i * K + 16 * kb);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const int row = min(tile[t] * 16 + i, N - 1);
-        const uint4_t* p = reinterpret_cast<const uint4_t*>(q + (size_t)row * K + (size_t)blk * kW8BlockK + 16 * kb);
-        r.a[t] = __builtin_nontemporal_load(p);
-        r.b[t] = __builtin_nontemporal_load(p + 4);
+        const uint32_t so = (uint32_t)(t * 16 * K + blk * kW8BlockK);
+        r.a[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo, so, kNtPolicy);
+        r.b[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + 64, so, kNtPolicy);
       }
     }
   };
@@ -114,6 +162,8 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+  // Pipeline: block blk+1's activations (LDS stage) and weights (registers)
+  // are requested before block blk's math; one wait + barrier per block.
   WRegs<F, NT> cur, nxt;
   copy_x(0, 0);
   fetch_w(0, cur);
@@ -130,6 +180,15 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
     const uint8_t* stage = xs + st * kStageBytes;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
+      // chunk of this k-step inside the 128-k block, matching the fragment
+      const int c = F == GFmt::W4 ? 4 * kb + w : 2 * kb + (w & 1) + 8 * (w >> 1);
+      static_assert(MT == 8, "fragment waits assume eight m-subtiles");
+      half8_t b[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int r = mt * 16 + i;
+        b[mt] = lds_read16(stage + r * kRowBytes + swz(r, c) * 16);
+      }
       half8_t a[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -146,15 +205,18 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
                         : i8x8_to_h8(cur.b[t].z, cur.b[t].w);
         }
       }
-      // chunk of this k-step inside the 128-k block, matching the fragment
-      const int c = F == GFmt::W4 ? 4 * kb + w : 2 * kb + (w & 1) + 8 * (w >> 1);
+      // The dequantization above overlaps the reads; the first half of the
+      // m-subtiles runs while the second half is still in flight.
+      lds_wait_first4(b);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int r = mt * 16 + i;
-        const half8_t b = *reinterpret_cast<const half8_t*>(stage + r * kRowBytes + swz(r, c) * 16);
+      for (int mt = 0; mt < MT / 2; ++mt)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], b, acc[t][mt]);
-      }
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], b[mt], acc[t][mt]);
+      lds_wait_last4(b);
+#pragma unroll
+      for (int mt = MT / 2; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], b[mt], acc[t][mt]);
     }
     if (more) cur = nxt;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's part of the next stage landed
