@@ -51,6 +51,58 @@ __device__ __forceinline__ uint4_t coherent_load16(const void* base, uint32_t by
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCoherentPolicy);
 }
 
+// Buffer over [base, base + bytes) (bytes clamped to the 31-bit record
+// count); accesses at or past the end read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int64_t bytes) {
+  const int nrec = (int)(bytes < 0 ? 0 : bytes > 0x7fffffff ? 0x7fffffff : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrec, kBufferRsrcWord3);
+}
+
+constexpr int kNtPolicy = 2;   // non-temporal: data streamed once
+
+// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane L's
+// bytes land at lds_base + 16 * L (out-of-range offsets land as zeros).
+// Kept out of kernel templates: with the builtin written inside one, the
+// host pass drops the kernel's launch stub.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0, 0);
+}
+
+// 16-byte LDS read issued as inline asm, for kernels that fill LDS with the
+// direct copies above: the compiler cannot tell such a copy into the next
+// stage from a read of the current one and waits for all of them (vmcnt(0))
+// before any LDS read it can see, which serializes the copy with the math.
+// These reads are invisible to it; lds_wait_first_half / lds_wait_rest must
+// complete them before use.
+__device__ __forceinline__ uint4_t lds_read16_asm(const uint8_t* p) {
+  const uint32_t a = (uint32_t)(size_t)((const __attribute__((address_space(3))) uint8_t*)p);
+  uint4_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+
+// For MT reads issued in order: wait until the first MT/2 have landed (LDS
+// reads return in order), then until all have; each wait is tied to the
+// fragments it completes so that no use moves above it.
+template <int MT>
+__device__ __forceinline__ void lds_wait_first_half(uint4_t (&b)[MT]) {
+  static_assert(MT == 2 || MT == 8, "fragment count");
+  if constexpr (MT == 8) {
+    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(b[0]));
+  }
+}
+template <int MT>
+__device__ __forceinline__ void lds_wait_rest(uint4_t (&b)[MT]) {
+  static_assert(MT == 2 || MT == 8, "fragment count");
+  if constexpr (MT == 8) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]));
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[1]));
+  }
+}
+
 __device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 

@@ -41,46 +41,8 @@ struct WRegs<GFmt::W8, NT> {
   uint4_t a[NT], b[NT];
 };
 
-// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane L's
-// bytes land at lds_base + 16 * L; offsets at or past the buffer's record
-// count read as zero.  Kept out of the kernel template: with the builtin
-// written inside it, the host pass drops the kernel's launch stub.
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* lds_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0, 0);
-}
-
-// Buffer over [base, base + bytes) (bytes clamped to the 31-bit record count).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int64_t bytes) {
-  const int nrec = (int)(bytes < 0 ? 0 : bytes > 0x7fffffff ? 0x7fffffff : bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrec, kBufferRsrcWord3);
-}
-
-constexpr int kNtPolicy = 2;   // non-temporal (streamed once)
-
 // LDS slot (16-byte chunk index inside a 256-byte row) of chunk c in row r.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 15); }
-
-// 16-byte LDS read issued as inline asm.  The compiler cannot tell the
-// buffer -> LDS copies of the next stage from reads of the current one, and
-// before any LDS read it can see it waits for every one of them (vmcnt(0)),
-// which serializes the copy with the math.  These reads are invisible to
-// it, so lds_wait_all() below must complete them before use.
-__device__ __forceinline__ half8_t lds_read16(const uint8_t* p) {
-  const uint32_t a = (uint32_t)(size_t)((const __attribute__((address_space(3))) uint8_t*)p);
-  half8_t v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
-  return v;
-}
-
-// Waits for the first four of eight fragment reads (lgkmcnt(4): LDS reads
-// return in order) or for all of them, tied to the fragments it completes so
-// that no use moves above it.
-__device__ __forceinline__ void lds_wait_first4(half8_t (&b)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
-}
-__device__ __forceinline__ void lds_wait_last4(half8_t (&b)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]));
-}
 
 template <GFmt F, int NT, int MT>
 __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restrict__ x, int M, int K,
@@ -182,12 +144,11 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
     for (int w = 0; w < 4; ++w) {
       // chunk of this k-step inside the 128-k block, matching the fragment
       const int c = F == GFmt::W4 ? 4 * kb + w : 2 * kb + (w & 1) + 8 * (w >> 1);
-      static_assert(MT == 8, "fragment waits assume eight m-subtiles");
-      half8_t b[MT];
+      uint4_t b[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int r = mt * 16 + i;
-        b[mt] = lds_read16(stage + r * kRowBytes + swz(r, c) * 16);
+        b[mt] = lds_read16_asm(stage + r * kRowBytes + swz(r, c) * 16);
       }
       half8_t a[NT];
 #pragma unroll
@@ -207,16 +168,16 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
       }
       // The dequantization above overlaps the reads; the first half of the
       // m-subtiles runs while the second half is still in flight.
-      lds_wait_first4(b);
+      lds_wait_first_half<MT>(b);
 #pragma unroll
       for (int mt = 0; mt < MT / 2; ++mt)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], b[mt], acc[t][mt]);
-      lds_wait_last4(b);
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], __builtin_bit_cast(half8_t, b[mt]), acc[t][mt]);
+      lds_wait_rest<MT>(b);
 #pragma unroll
       for (int mt = MT / 2; mt < MT; ++mt)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], b[mt], acc[t][mt]);
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], __builtin_bit_cast(half8_t, b[mt]), acc[t][mt]);
     }
     if (more) cur = nxt;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's part of the next stage landed

@@ -275,7 +275,8 @@ constexpr int flat_max_ksw() { return NB <= (F == WFmt::W4 ? 12 : 8) ? 16 : 8; }
 // Waves per SIMD each instantiation must reach: the wide-N plans launch
 // about 4.25 waves per SIMD (e.g. 1088 four-wave workgroups for 5120->17408),
 // so NB <= 10 is held to 96 VGPRs (five waves per SIMD) and the whole grid is
-// resident at once instead of leaving a second launch wave.
+// resident at once instead of leaving a second launch wave.  The fused
+// RMSNorm / SiLU·up prologues fit in the same budget (no scratch).
 template <int NB, WFmt F>
 constexpr int flat_min_waves() { return NB <= (F == WFmt::W4 ? 10 : 6) ? 5 : 1; }
 
@@ -332,7 +333,7 @@ __device__ __forceinline__ uint4_t silu_mul8(uint4_t gv, uint4_t uv) {
 }
 
 template <int NB, int MM, WFmt F, XMode XM = XMode::Plain>
-__global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (XM == XMode::Plain ? flat_min_waves<NB, F>() : 1)) void gemv_flat_kernel(
+__global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F>())) void gemv_flat_kernel(
     const half_t* __restrict__ x, int M, int K, const void* __restrict__ wsrc, const void* __restrict__ wmeta,
     const half_t* __restrict__ bias, int N, int g_shift, half_t* y, int S,
     float4_t* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt, FuseArgs fz) {
