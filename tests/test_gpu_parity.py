@@ -280,6 +280,30 @@ def test_w4a16_rejects_unsupported_shapes(gpu):
         wq.CompressedLinearBackend('marlin').prepare(layer, 'p.weight')
 
 
+@pytest.mark.parametrize('fmt', ['w4', 'w8'])
+def test_prefill_gemm_activations_beyond_2gib(gpu, fmt):
+    """x of 65601 x 17408 fp16 (2.28 GB, past 2^31 bytes): the GEMM addresses it through
+    per-workgroup buffer bases with 32-bit offsets; rows at the start, the middle and the
+    end, including the partial last 128-row block, checked against the oracle."""
+    m, k, n = 65601, 17408, 64
+    rows = np.array([0, 1, 127, 128, 32767, 40000, 65535, 65536, 65599, 65600])
+    x = torch.randn(m, k, device=gpu, dtype=torch.float16)
+    xr = host(x[torch.from_numpy(rows).to(gpu)])
+    if fmt == 'w4':
+        name = 'mlp.down_proj.weight'
+        weights, _ = synth.w4_case(n, k, 1, seed=21, name=name)
+        backend, layer = prepared_w4(weights, name, gpu)
+        y = host(backend.linear(x, layer, name))
+        expected = qdq.qdq_linear(xr, weights, name)
+    else:
+        _, q, s, _ = synth.int8_case(n, k, 1, seed=22)
+        y = host(_native.w8a16_linear(x, dev(q, gpu), dev(s, gpu)))
+        expected = int8_ref(xr, q, s)
+    del x
+    check_parity(y[rows], expected, f'{fmt} prefill m={m} k={k} n={n} rows')
+    assert np.isfinite(y).all()
+
+
 # ------------------------------------------------------------------ INT8 (W8A16)
 
 def int8_ref(x, q, s, bias=None):
