@@ -34,6 +34,10 @@ int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uin
 
 // Largest M served by the MFMA GEMV (4 chunks of 16 activation rows).
 constexpr int64_t kSkinnyMaxM = 64;
+// Largest k of the prefill GEMMs: they address a workgroup's 128 x rows with
+// 32-bit buffer offsets (up to 248 k bytes).  Longer rows run the skinny
+// kernels 64 rows at a time.
+constexpr int64_t kGemmMaxK = 1 << 24;
 
 namespace {
 
@@ -89,6 +93,16 @@ extern "C" int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const vo
     return launch_w4_skinny(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
                             reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, workspace,
                             workspace_bytes, as_stream(stream));
+  if (k > kGemmMaxK) {
+    for (int64_t r = 0; r < m; r += kSkinnyMaxM) {
+      const int64_t mr = m - r < kSkinnyMaxM ? m - r : kSkinnyMaxM;
+      const int rc = launch_w4_skinny(xh + r * k, (int)mr, (int)k, reinterpret_cast<const uint4_t*>(tiles),
+                                      reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh + r * n,
+                                      workspace, workspace_bytes, as_stream(stream));
+      if (rc != WQ_OK) return rc;
+    }
+    return WQ_OK;
+  }
   return launch_w4_gemm(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
                         reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
 }
@@ -128,7 +142,7 @@ extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const in
   const half_t* sh = reinterpret_cast<const half_t*>(scale);
   const half_t* bh = reinterpret_cast<const half_t*>(bias);
   half_t* yh = reinterpret_cast<half_t*>(y);
-  if (k % kW8BlockK != 0 || !aligned16(x) || !aligned16(qweight))
+  if (k % kW8BlockK != 0 || !aligned16(x) || !aligned16(qweight) || (m > kSkinnyMaxM && k > kGemmMaxK))
     return launch_w8_generic(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
   if (m <= kSkinnyMaxM)
     return launch_w8_skinny(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, workspace, workspace_bytes,
