@@ -160,16 +160,25 @@ def test_w4a16_prefill_full_shapes_sampled_rows(gpu, k, n):
     assert np.isfinite(y).all()
 
 
-def test_w4a16_lm_head_sampled_columns(gpu):
-    """config 4's lm_head 5120->151936 at M in {1, 32}: 4096 output columns checked."""
-    name = 'lm_head.weight'
-    weights, x = synth.w4_case(151936, 5120, 32, seed=9, name=name)
+CONFIG4_M = (1, 8, 32, 128, 512)
+
+
+@pytest.mark.parametrize('name,n,ncols', [('self_attn.qkv_proj.weight', 7168, None),
+                                          ('mlp.gate_up_proj.weight', 34816, 4096),
+                                          ('lm_head.weight', 151936, 4096)])
+def test_w4a16_config4_batch_sweep(gpu, name, n, ncols):
+    """config 4: fused QKV 5120->7168, gate_up 5120->34816 and lm_head 5120->151936 at
+    M in {1, 8, 32, 128, 512} (GEMV, skinny and GEMM paths); every output column of
+    QKV, 4096 sampled columns of the wider two."""
+    k = 5120
+    weights, x = synth.w4_case(n, k, max(CONFIG4_M), seed=9 + n % 7, name=name)
     backend, layer = prepared_w4(weights, name, gpu)
-    cols = np.sort(np.random.default_rng(4).choice(151936, size=4096, replace=False))
+    cols = np.arange(n) if ncols is None else np.sort(np.random.default_rng(4).choice(n, size=ncols, replace=False))
     w_cols = qdq.decode_rows(weights, name, cols)
-    for m in (1, 32):
+    for m in CONFIG4_M:
         y = host(backend.linear(dev(x[:m], gpu), layer, name))
-        check_parity(y[:, cols], qdq.linear_fp32(x[:m], w_cols), f'w4 lm_head m={m}')
+        assert y.shape == (m, n)
+        check_parity(y[:, cols], qdq.linear_fp32(x[:m], w_cols), f'w4 {name} {k}->{n} m={m}')
 
 
 def test_w4a16_repeat_calls_are_bitwise_identical(gpu):
