@@ -25,6 +25,8 @@ Also in the same JSON line:
   they run on; ``traffic`` from the committed rocprofv3 counter summary;
 * ``decode_step_kernels``: the same timing for every kernel of the step;
 * ``prefill``: the M=4096 W4A16 GEMM (configs[2]) per shape, TFLOP/s;
+* ``batch_sweep``: fused QKV, fused gate_up and a W4 lm_head at
+  M in {1, 8, 32, 128, 512}, GB/s and TFLOP/s per launch;
 * ``int8``: configs[0]'s INT8 weight on the GPU: weight-only W8A16 decode GB/s,
   and W8A8 (``int8_gemm``) decode GB/s and M=4096 TOPS vs the int8 MFMA peak;
 * ``copy_ceiling``: a device-to-device copy's GB/s on the same box;
@@ -413,6 +415,41 @@ def main() -> int:
                             'tflops': round(tflops, 1), 'frac_fp16_mfma': round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)})
             del g, yp
         result['prefill'] = prefill
+
+        # fused QKV and gate_up (every layer's weights in one graph,
+        # so the 256 MB Infinity Cache cannot serve repeats) and a W4 lm_head
+        # 5120->151936 (random tiles, 389 MB), at M in {1, 8, 32, 128, 512}.
+        vocab = cfg.vocab_size
+        lm_tb, lm_mb = native.w4_repack_size(vocab, HIDDEN, GROUP)
+        lm_tiles = torch.randint(0, 256, (lm_tb,), dtype=torch.uint8, device=device)
+        lm_meta = torch.randint(0, 256, (lm_mb,), dtype=torch.uint8, device=device)
+        lm_meta.view(torch.float16)[:] = 0.001   # finite scales; the zero words take the same bits
+        sweep = []
+        for name, n, ws_list in [('self_attn.qkv_proj', QKV, None), ('mlp.gate_up_proj', GATE_UP, None),
+                                 ('lm_head (W4)', vocab, [lm_tiles, lm_meta])]:
+            for m in (1, 8, 32, 128, 512):
+                xm = torch.randn(m, HIDDEN, device=device).half()
+                ym = torch.empty(m, n, device=device, dtype=torch.float16)
+                wsz = native.w4a16_workspace_size(m, n, HIDDEN, GROUP)
+                wsb = torch.zeros(max(wsz, 1), dtype=torch.uint8, device=device)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    if ws_list is None:
+                        for w in layers:
+                            pr = w[name + '._prepared']
+                            native.w4a16_linear(xm, pr.tiles, pr.meta, n, GROUP, out=ym, workspace=wsb)
+                    else:
+                        native.w4a16_linear(xm, ws_list[0], ws_list[1], n, GROUP, out=ym, workspace=wsb)
+                launches = len(layers) if ws_list is None else 1
+                per = time_graph(torch, g, 5) / launches
+                b = w4_bytes(m, n, HIDDEN)
+                tf = 2 * m * n * HIDDEN / per / 1e12
+                sweep.append({'op': name, 'shape': f'{HIDDEN}->{n}', 'M': m, 'us': round(per * 1e6, 2),
+                              'gbs': round(b / per / 1e9, 1), 'frac_hbm': round(b / per / 1e9 / HBM_PEAK_GBS, 4),
+                              'tflops': round(tf, 1), 'frac_fp16_mfma': round(tf / FP16_MFMA_PEAK_TFLOPS, 4)})
+                del g, xm, ym, wsb
+        result['batch_sweep'] = sweep
+        del lm_tiles, lm_meta
 
         # INT8 variants on configs[0]'s weight (5120 x 5120, N(0, 0.02), per-channel
         # symmetric INT8): weight-only W8A16 decode, and W8A8 (int8_gemm) decode

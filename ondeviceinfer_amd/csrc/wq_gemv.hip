@@ -603,19 +603,26 @@ struct SkinnyCfg {
 template <int MC>
 constexpr int skinny_unroll() { return MC == 1 ? 4 : 2; }
 
-// Largest k-split per workgroup: 16 waves for M <= 16; 4 above, where a
-// wave needs more than 128 VGPRs and 1024-thread groups would spill.
-template <int MC>
-constexpr int skinny_max_ksw() { return MC == 1 ? 16 : 4; }
+// Largest k-split per workgroup: 16 waves for M <= 16 with one tile per
+// wave, 8 with more tiles (their registers exceed a 1024-thread group's
+// 128 VGPRs); 4 above M = 16.
+template <int MC, int TPW>
+constexpr int skinny_max_ksw() { return MC == 1 ? (TPW == 1 ? 16 : 8) : 4; }
 
 // Enough waves to cover the machine (256 CUs) several times over while each
-// wave keeps at least two k blocks.
-SkinnyCfg pick_skinny(int ntile, int nblk, int mc) {
+// wave keeps at least two k blocks.  W4 waves take 2 tiles (4 from 1024
+// tiles on) so that each activation fragment read from L2 feeds 2 or 4
+// tiles' MFMAs, and at least 2 waves split k: from sweeps of the fused
+// QKV, gate_up and lm_head shapes at M = 8 .. 64 on MI355X (gate_up M = 8:
+// 42 -> 33 us, lm_head M = 32: 229 -> 155 us against one tile per wave).
+SkinnyCfg pick_skinny(int ntile, int nblk, int mc, bool w4) {
   SkinnyCfg c{mc >= 2 ? 2 : 1, 1};
-  const int max_ksw = mc == 1 ? 16 : 4;
+  if (w4) c.tpw = ntile >= 1024 ? 4 : 2;
+  const int max_ksw = mc == 1 ? (c.tpw == 1 ? 16 : 8) : 4;
   const int groups = (ntile + c.tpw - 1) / c.tpw;
   int ksw = 1;
   while (ksw < max_ksw && groups * ksw < 2048 && nblk / (ksw * 2) >= 2) ksw *= 2;
+  if (w4 && ksw == 1 && nblk >= 4) ksw = 2;
   c.ksw = ksw;
   return c;
 }
@@ -638,9 +645,11 @@ int launch_w4_skinny_k(int ksw, const half_t* x, int M, int K, const uint4_t* ti
     case 2: return launch_w4_skinny_cfg<MC, TPW, 2>(x, M, K, tiles, meta, N, G, y, s);
     case 4: return launch_w4_skinny_cfg<MC, TPW, 4>(x, M, K, tiles, meta, N, G, y, s);
     default:
-      if constexpr (skinny_max_ksw<MC>() >= 16) {
+      if constexpr (skinny_max_ksw<MC, TPW>() >= 16) {
         if (ksw == 8) return launch_w4_skinny_cfg<MC, TPW, 8>(x, M, K, tiles, meta, N, G, y, s);
         return launch_w4_skinny_cfg<MC, TPW, 16>(x, M, K, tiles, meta, N, G, y, s);
+      } else if constexpr (skinny_max_ksw<MC, TPW>() >= 8) {
+        return launch_w4_skinny_cfg<MC, TPW, 8>(x, M, K, tiles, meta, N, G, y, s);
       } else {
         return launch_w4_skinny_cfg<MC, TPW, 4>(x, M, K, tiles, meta, N, G, y, s);
       }
@@ -665,7 +674,7 @@ int launch_w8_skinny_k(int ksw, const half_t* x, int M, int K, const int8_t* q, 
     case 2: return launch_w8_skinny_cfg<MC, TPW, 2>(x, M, K, q, scale, bias, N, y, s);
     case 4: return launch_w8_skinny_cfg<MC, TPW, 4>(x, M, K, q, scale, bias, N, y, s);
     default:
-      if constexpr (skinny_max_ksw<MC>() >= 16) {
+      if constexpr (skinny_max_ksw<MC, TPW>() >= 16) {
         if (ksw == 8) return launch_w8_skinny_cfg<MC, TPW, 8>(x, M, K, q, scale, bias, N, y, s);
         return launch_w8_skinny_cfg<MC, TPW, 16>(x, M, K, q, scale, bias, N, y, s);
       } else {
@@ -810,12 +819,17 @@ int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const 
     if (rc != kNotApplicable) return rc;
   }
   const int mc = (M + 15) / 16;
-  const SkinnyCfg c = pick_skinny((N + 15) / 16, K / kW4BlockK, mc);
+  const SkinnyCfg c = pick_skinny((N + 15) / 16, K / kW4BlockK, mc, true);
+  const bool t4 = c.tpw == 4;
   switch (mc) {
-    case 1: return launch_w4_skinny_k<1, 1>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
-    case 2: return launch_w4_skinny_k<2, 2>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
-    case 3: return launch_w4_skinny_k<3, 2>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
-    default: return launch_w4_skinny_k<4, 2>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
+    case 1: return t4 ? launch_w4_skinny_k<1, 4>(c.ksw, x, M, K, tiles, meta, N, G, y, s)
+                      : launch_w4_skinny_k<1, 2>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
+    case 2: return t4 ? launch_w4_skinny_k<2, 4>(c.ksw, x, M, K, tiles, meta, N, G, y, s)
+                      : launch_w4_skinny_k<2, 2>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
+    case 3: return t4 ? launch_w4_skinny_k<3, 4>(c.ksw, x, M, K, tiles, meta, N, G, y, s)
+                      : launch_w4_skinny_k<3, 2>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
+    default: return t4 ? launch_w4_skinny_k<4, 4>(c.ksw, x, M, K, tiles, meta, N, G, y, s)
+                       : launch_w4_skinny_k<4, 2>(c.ksw, x, M, K, tiles, meta, N, G, y, s);
   }
 }
 
@@ -826,7 +840,7 @@ int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_
     if (rc != kNotApplicable) return rc;
   }
   const int mc = (M + 15) / 16;
-  const SkinnyCfg c = pick_skinny((N + 15) / 16, K / kW8BlockK, mc);
+  const SkinnyCfg c = pick_skinny((N + 15) / 16, K / kW8BlockK, mc, false);
   switch (mc) {
     case 1: return launch_w8_skinny_k<1, 1>(c.ksw, x, M, K, q, scale, bias, N, y, s);
     case 2: return launch_w8_skinny_k<2, 2>(c.ksw, x, M, K, q, scale, bias, N, y, s);

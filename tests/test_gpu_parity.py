@@ -114,6 +114,17 @@ def test_w4a16_linear_parity_small(gpu, m, n, k):
     check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 m={m} n={n} k={k}')
 
 
+@pytest.mark.parametrize('m', [5, 9, 16, 17, 40, 64])
+def test_w4a16_skinny_four_tiles_per_wave(gpu, m):
+    """M = 5 .. 64 over 1025 tiles (four tiles per wave from 1024 on, the last
+    group partial): every output against the oracle."""
+    name = 'mlp.gate_up_proj.weight'
+    weights, x = synth.w4_case(16400, 1024, m, seed=m + 100, name=name)
+    backend, layer = prepared_w4(weights, name, gpu)
+    y = backend.linear(dev(x, gpu), layer, name)
+    check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 skinny m={m} n=16400')
+
+
 @pytest.mark.parametrize('ksw,split', [('1', '1'), ('3', '1'), ('16', '1'), ('3', '2'), ('2', '4')])
 def test_w4a16_decode_wave_split_override(gpu, monkeypatch, ksw, split):
     """Uneven block counts per wave and per k-split (tuning overrides)."""
