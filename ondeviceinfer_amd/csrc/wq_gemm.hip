@@ -10,11 +10,11 @@
 //  * each wave loads its weight tiles straight from HBM into registers one
 //    block ahead (the W4 tile layout already is the MFMA A-fragment order)
 //    and dequantizes them there, one tile at a time;
+//  * NT x MT x 4 MFMA v_mfma_f32_16x16x32_f16 accumulate in fp32.
 // Every load goes through a buffer resource with a wave-uniform base and a
 // 32-bit lane offset, so no 64-bit per-lane address stays live and the
 // accumulators fit without spills; rows past M and tiles past N fall
 // outside the buffers and read as zero.
-//  * NT x MT x 4 MFMA v_mfma_f32_16x16x32_f16 accumulate in fp32.
 // W4 weights are dequantized with their group scale, fp16((q - z) * s): the
 // oracle's fp16 weight bit for bit.  INT8 weights enter as exact fp16 q and
 // the per-row scale multiplies the fp32 sum in the epilogue.
