@@ -61,6 +61,24 @@ int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t kv_heads, 
                         uint16_t* key_cache, uint16_t* value_cache, int64_t max_seq, float scale, uint16_t* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Prefill (tokens >= 1, batch 1) q/k RMSNorm + RoPE with the cache append:
+ *   qkv          [tokens, q_heads*128 | kv_heads*128 | kv_heads*128] fused
+ *                projection output, row t at position start + t
+ *   q/k_norm     per-head RMSNorm weights [128] (NULL: no norm)
+ *   cos/sin_rows [tokens, 128] fp16 RoPE rows of those positions
+ *   key/value_cache [kv_heads, max_seq, 128] fp16; rows start .. start+tokens-1
+ *                receive the normalized, rotated k and the v
+ *   q_out        [q_heads, tokens, 128] normalized, rotated q
+ * Same numerics per element as wq_decode_attention's prologue.  Replaces:
+ * the q/k rms_norm + apply_rotary_pos_emb of a multi-token forward
+ * (quantized_model.py:177-184, layers.py:64-80) and the cache.update inside
+ * its cached attention (quantized_model.py:186-195, attention.py:35-85,
+ * cache.py:60-80).  start + tokens <= max_seq. */
+int wq_prefill_qk_rope(const uint16_t* qkv, int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                       const uint16_t* q_norm_weight, const uint16_t* k_norm_weight, float eps,
+                       const uint16_t* cos_rows, const uint16_t* sin_rows, int64_t start, uint16_t* key_cache,
+                       uint16_t* value_cache, int64_t max_seq, uint16_t* q_out, void* stream);
+
 /* Workspace bytes for wq_lm_head with token != NULL (the per-wave argmax
  * candidates; no initialization needed). */
 int wq_lm_head_workspace_size(int64_t k, int64_t vocab, size_t* bytes);

@@ -62,6 +62,7 @@ _SIGNATURES = {
     'wq_decode_attention_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
     'wq_decode_attention': [_P, _I64, _I64, _I64, _P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _I64,
                             ctypes.c_float, _P, _P, ctypes.c_size_t, _P],
+    'wq_prefill_qk_rope': [_P, _I64, _I64, _I64, _I64, _P, _P, ctypes.c_float, _P, _P, _I64, _P, _P, _I64, _P, _P],
     'wq_lm_head_workspace_size': [_I64, _I64, _SIZE_P],
     'wq_lm_head': [_P, _I64, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
 }
@@ -510,6 +511,39 @@ def decode_attention(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: tor
           _ptr(cos_table), _ptr(sin_table), _ptr(position), _ptr(key_cache), _ptr(value_cache), max_seq,
           float(scale), _ptr(out), ws_ptr, ws_bytes, _stream(device))
     return out
+
+
+def prefill_qk_rope(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: torch.Tensor | None,
+                    k_norm: torch.Tensor | None, eps: float, cos_rows: torch.Tensor, sin_rows: torch.Tensor,
+                    start: int, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                    q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k RMSNorm + RoPE of ``tokens`` rows of a fused QKV projection (batch 1)
+    at positions ``start ..``; k and v land in rows ``start ..`` of the caches
+    (``[kv_heads, max_seq, head_dim]`` fp16); returns q as
+    ``[q_heads, tokens, head_dim]``."""
+    device = _require_gpu(qkv, q_norm, k_norm, cos_rows, sin_rows, key_cache, value_cache, q_out)
+    if key_cache.dim() != 3 or key_cache.shape != value_cache.shape or key_cache.shape[0] != kv_heads:
+        raise ValueError(f'caches must be [kv_heads={kv_heads}, max_seq, head_dim], got {tuple(key_cache.shape)}')
+    _, max_seq, head_dim = key_cache.shape
+    for t, name in ((key_cache, 'key_cache'), (value_cache, 'value_cache')):
+        _check(t, torch.float16, (kv_heads, max_seq, head_dim), name)
+    if qkv.dim() != 2:
+        raise ValueError(f'qkv must be [tokens, (q_heads + 2 kv_heads) * head_dim], got {tuple(qkv.shape)}')
+    tokens = qkv.shape[0]
+    _check(qkv, torch.float16, (tokens, (q_heads + 2 * kv_heads) * head_dim), 'qkv')
+    for t, name in ((cos_rows, 'cos_rows'), (sin_rows, 'sin_rows')):
+        _check(t, torch.float16, (tokens, head_dim), name)
+    for t, name in ((q_norm, 'q_norm'), (k_norm, 'k_norm')):
+        if t is not None:
+            _check(t, torch.float16, (head_dim,), name)
+    if q_out is None:
+        q_out = torch.empty(q_heads, tokens, head_dim, dtype=torch.float16, device=device)
+    else:
+        _check(q_out, torch.float16, (q_heads, tokens, head_dim), 'q_out')
+    _call('wq_prefill_qk_rope', _ptr(qkv), tokens, q_heads, kv_heads, head_dim, _ptr(q_norm), _ptr(k_norm),
+          float(eps), _ptr(cos_rows), _ptr(sin_rows), int(start), _ptr(key_cache), _ptr(value_cache), max_seq,
+          _ptr(q_out), _stream(device))
+    return q_out
 
 
 def lm_head_workspace_size(k: int, vocab: int) -> int:

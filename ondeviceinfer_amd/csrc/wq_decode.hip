@@ -414,6 +414,41 @@ size_t attention_workspace_bytes(int64_t H, int64_t KV, int64_t max_seq) {
   return nc <= 1 ? 0 : align256((size_t)KV * nc * g * 2 * 4) + (size_t)KV * nc * g * kHeadDim * 4;
 }
 
+// Prefill counterpart of the decode kernel's prologue, for `tokens` rows of
+// a fused [q | k | v] projection at positions start .. start + tokens - 1:
+// per (token, head) one wave (lane l holds d = 2l, 2l+1) applies the head's
+// RMSNorm and RoPE with norm_rope_pair (q and k), writes q as [head][token][d]
+// (the layout attention reads) and appends k and v to the cache rows.
+// grid = (tokens, ceil((q_heads + 2 kv_heads) / 4)), 256 threads.
+__global__ __launch_bounds__(256) void prefill_qk_rope_kernel(const half_t* __restrict__ qkv, int T, int H, int KV,
+                                                              const half_t* __restrict__ qn_w,
+                                                              const half_t* __restrict__ kn_w, float eps,
+                                                              const half_t* __restrict__ cos_t,
+                                                              const half_t* __restrict__ sin_t, int start,
+                                                              half_t* __restrict__ kc, half_t* __restrict__ vc,
+                                                              int max_seq, half_t* __restrict__ q_out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x;
+  const int hh = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (hh >= H + 2 * KV) return;
+  const size_t row = (size_t)t * (H + 2 * KV) * kHeadDim;
+  const half2_t v = as_h2(reinterpret_cast<const uint32_t*>(qkv + row + (size_t)hh * kHeadDim)[lane]);
+  if (hh >= H + KV) {
+    const int h = hh - H - KV;
+    reinterpret_cast<uint32_t*>(vc + ((size_t)h * max_seq + start + t) * kHeadDim)[lane] = as_u32(v);
+    return;
+  }
+  const bool is_q = hh < H;
+  const half_t* nw_p = is_q ? qn_w : kn_w;
+  const half2_t nw = nw_p ? as_h2(reinterpret_cast<const uint32_t*>(nw_p)[lane]) : half2_t{};
+  const half2_t c2 = as_h2(reinterpret_cast<const uint32_t*>(cos_t + (size_t)t * kHeadDim)[lane]);
+  const half2_t s2 = as_h2(reinterpret_cast<const uint32_t*>(sin_t + (size_t)t * kHeadDim)[lane]);
+  const half2_t r = norm_rope_pair(v, nw_p != nullptr, nw, eps, c2, s2, lane);
+  half_t* dst = is_q ? q_out + ((size_t)hh * T + t) * kHeadDim
+                     : kc + ((size_t)(hh - H) * max_seq + start + t) * kHeadDim;
+  reinterpret_cast<uint32_t*>(dst)[lane] = as_u32(r);
+}
+
 int attention_shape_check(int64_t H, int64_t KV, int64_t head_dim, int64_t max_seq) {
   WQ_REQUIRE(H > 0 && KV > 0 && max_seq > 0, WQ_ERR_INVALID_ARGUMENT, "q_heads, kv_heads and max_seq must be positive");
   WQ_REQUIRE(head_dim == kHeadDim, WQ_ERR_UNSUPPORTED, "decode attention is built for head_dim 128 (got %lld)",
@@ -524,4 +559,33 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
     return check_launch("decode_attention_merge");
   }
   return check_launch("decode_attention");
+}
+
+extern "C" int wq_prefill_qk_rope(const uint16_t* qkv, int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                                  int64_t head_dim, const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
+                                  float eps, const uint16_t* cos_rows, const uint16_t* sin_rows, int64_t start,
+                                  uint16_t* key_cache, uint16_t* value_cache, int64_t max_seq, uint16_t* q_out,
+                                  void* stream) {
+  if (tokens == 0) return WQ_OK;
+  WQ_REQUIRE(tokens > 0 && tokens <= 0x7fffffff, WQ_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
+  WQ_REQUIRE(q_heads > 0 && kv_heads > 0 && max_seq > 0 && q_heads + 2 * kv_heads <= 4 * 65535,
+             WQ_ERR_INVALID_ARGUMENT, "bad head counts or max_seq");
+  WQ_REQUIRE(head_dim == kHeadDim, WQ_ERR_UNSUPPORTED, "prefill q/k RoPE is built for head_dim 128 (got %lld)",
+             (long long)head_dim);
+  WQ_REQUIRE(start >= 0 && start + tokens <= max_seq && max_seq <= 0x7fffffff, WQ_ERR_INVALID_ARGUMENT,
+             "KV cache capacity exceeded: rows %lld .. %lld of %lld", (long long)start, (long long)(start + tokens),
+             (long long)max_seq);
+  WQ_REQUIRE(qkv && cos_rows && sin_rows && key_cache && value_cache && q_out, WQ_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
+  WQ_REQUIRE(((uintptr_t)qkv | (uintptr_t)cos_rows | (uintptr_t)sin_rows | (uintptr_t)key_cache |
+              (uintptr_t)value_cache | (uintptr_t)q_out | (uintptr_t)q_norm_weight | (uintptr_t)k_norm_weight) % 4 == 0,
+             WQ_ERR_INVALID_ARGUMENT, "operands must be 4-byte aligned");
+  const dim3 grid((unsigned)tokens, (unsigned)((q_heads + 2 * kv_heads + 3) / 4));
+  hipLaunchKernelGGL(prefill_qk_rope_kernel, grid, dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const half_t*>(qkv), (int)tokens, (int)q_heads, (int)kv_heads,
+                     reinterpret_cast<const half_t*>(q_norm_weight), reinterpret_cast<const half_t*>(k_norm_weight),
+                     eps, reinterpret_cast<const half_t*>(cos_rows), reinterpret_cast<const half_t*>(sin_rows),
+                     (int)start, reinterpret_cast<half_t*>(key_cache), reinterpret_cast<half_t*>(value_cache),
+                     (int)max_seq, reinterpret_cast<half_t*>(q_out));
+  return check_launch("prefill_qk_rope");
 }

@@ -134,22 +134,42 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     residual = hidden_states
     states = rms_norm(hidden_states, weights['input_layernorm.weight'], eps)
     batch_size, query_length, _ = states.shape
+    qkv = None
     if linear_backend is not None and _has_prepared(weights, QKV_FUSED):
         qkv = linear(states, QKV_FUSED)
-        query, key, value = qkv.split((hq * d, hkv * d, hkv * d), dim=-1)
+    if (qkv is not None and batch_size == 1 and d == 128 and qkv.is_cuda and qkv.dtype == torch.float16
+            and isinstance(cache, ResidentKVCache) and cache.batch_size == 1
+            and cos.dtype == torch.float16 and tuple(cos.shape) == (1, query_length, d)):
+        # Resident batch-1 cache: q/k norm, RoPE and the cache append in one
+        # launch (same per-element arithmetic as the steps below).
+        start = cache.get_seq_length(layer_idx)
+        end = start + query_length
+        if end > cache.max_seq_len:
+            raise ValueError(f'KV cache capacity exceeded: requested {end}, capacity {cache.max_seq_len}')
+        query = _native.prefill_qk_rope(
+            qkv.view(query_length, -1), hq, hkv, weights['self_attn.q_norm.weight'],
+            weights['self_attn.k_norm.weight'], eps, cos[0], sin[0], start, cache.key_cache[layer_idx][0],
+            cache.value_cache[layer_idx][0]).unsqueeze(0)
+        cache.lengths[layer_idx] = end
+        attention_output = cached_scaled_dot_product_attention(
+            query, cache.key_cache[layer_idx][:, :, :end], cache.value_cache[layer_idx][:, :, :end],
+            layer_idx=layer_idx, cache=None, attention_mask=None, dropout_p=0.0)
     else:
-        query = linear(states, 'self_attn.q_proj.weight')
-        key = linear(states, 'self_attn.k_proj.weight')
-        value = linear(states, 'self_attn.v_proj.weight')
-    query = query.reshape(batch_size, query_length, hq, d)
-    key = key.reshape(batch_size, query_length, hkv, d)
-    value = value.reshape(batch_size, query_length, hkv, d)
-    query = rms_norm(query, weights['self_attn.q_norm.weight'], eps).transpose(1, 2)
-    key = rms_norm(key, weights['self_attn.k_norm.weight'], eps).transpose(1, 2)
-    value = value.transpose(1, 2)
-    query, key = apply_rotary_pos_emb(query, key, cos, sin)
-    attention_output = cached_scaled_dot_product_attention(query, key, value, layer_idx=layer_idx, cache=cache,
-                                                           attention_mask=None, dropout_p=0.0)
+        if qkv is not None:
+            query, key, value = qkv.split((hq * d, hkv * d, hkv * d), dim=-1)
+        else:
+            query = linear(states, 'self_attn.q_proj.weight')
+            key = linear(states, 'self_attn.k_proj.weight')
+            value = linear(states, 'self_attn.v_proj.weight')
+        query = query.reshape(batch_size, query_length, hq, d)
+        key = key.reshape(batch_size, query_length, hkv, d)
+        value = value.reshape(batch_size, query_length, hkv, d)
+        query = rms_norm(query, weights['self_attn.q_norm.weight'], eps).transpose(1, 2)
+        key = rms_norm(key, weights['self_attn.k_norm.weight'], eps).transpose(1, 2)
+        value = value.transpose(1, 2)
+        query, key = apply_rotary_pos_emb(query, key, cos, sin)
+        attention_output = cached_scaled_dot_product_attention(query, key, value, layer_idx=layer_idx,
+                                                               cache=cache, attention_mask=None, dropout_p=0.0)
     attention_output = attention_output.transpose(1, 2).contiguous().view(batch_size, query_length, hq * d)
     attention_output = linear(attention_output, 'self_attn.o_proj.weight')
     hidden_states = residual + attention_output

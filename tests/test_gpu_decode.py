@@ -133,6 +133,46 @@ def test_decode_attention_matches_oracle(nat, h, kv, max_seq, positions):
 
 
 
+@pytest.mark.parametrize('tokens,start,h,kv,with_norm', [(37, 5, 40, 8, True), (1, 0, 8, 8, True),
+                                                          (300, 100, 64, 8, False), (4096, 0, 40, 8, True)])
+def test_prefill_qk_rope_matches_oracle(nat, tokens, start, h, kv, with_norm):
+    """Multi-token q/k RMSNorm + RoPE + cache append (one launch) against the
+    oracle's rms_norm / apply_rope; v copied bit for bit; other cache rows kept."""
+    d, eps = 128, 1e-6
+    rng = np.random.default_rng(tokens + start + h)
+    max_seq = start + tokens + 3
+    qkv = rng.standard_normal((tokens, (h + 2 * kv) * d), dtype=np.float32).astype(np.float16)
+    qn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float16)
+    kn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float16)
+    cos, sin = qwen3.rotary_tables(d, 1e6, np.arange(start, start + tokens))
+    kc = torch.full((kv, max_seq, d), float('nan'), dtype=torch.float16, device='cuda')
+    vc = torch.full((kv, max_seq, d), float('nan'), dtype=torch.float16, device='cuda')
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    q = nat.prefill_qk_rope(dev(qkv), h, kv, dev(qn) if with_norm else None, dev(kn) if with_norm else None, eps,
+                            dev(cos), dev(sin), start, kc, vc)
+    torch.cuda.synchronize()
+    x = qkv.reshape(tokens, h + 2 * kv, d)
+    qr, kr, vr = x[:, :h], x[:, h:h + kv], x[:, h + kv:]
+    if with_norm:
+        qr, kr = qwen3.rms_norm(qr, qn, eps), qwen3.rms_norm(kr, kn, eps)
+    q_ref = qwen3.apply_rope(qr.transpose(1, 0, 2), cos, sin)
+    k_ref = qwen3.apply_rope(kr.transpose(1, 0, 2), cos, sin)
+    _close(q.cpu().numpy(), q_ref)
+    kcn, vcn = kc.cpu().numpy(), vc.cpu().numpy()
+    _close(kcn[:, start:start + tokens], k_ref)
+    assert np.array_equal(vcn[:, start:start + tokens], vr.transpose(1, 0, 2))
+    for c in (kcn, vcn):
+        assert np.isnan(c[:, :start]).all() and np.isnan(c[:, start + tokens:]).all()
+
+
+def test_prefill_qk_rope_rejects_capacity_overflow(nat):
+    kc = torch.zeros((8, 16, 128), dtype=torch.float16, device='cuda')
+    qkv = torch.zeros((4, 56 * 128), dtype=torch.float16, device='cuda')
+    cs = torch.zeros((4, 128), dtype=torch.float16, device='cuda')
+    with pytest.raises(ValueError, match='capacity'):
+        nat.prefill_qk_rope(qkv, 40, 8, None, None, 1e-6, cs, cs, 13, kc, kc.clone())
+
+
 def test_decode_attention_without_norms(nat):
     case = AttnCase(16, 4, 500, seed=9, norms=False)
     ws = torch.zeros(nat.decode_attention_workspace_size(16, 4, 128, 500), dtype=torch.uint8, device='cuda')
