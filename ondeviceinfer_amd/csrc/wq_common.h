@@ -86,18 +86,22 @@ __device__ __forceinline__ uint4_t lds_read16_asm(const uint8_t* p) {
 // fragments it completes so that no use moves above it.
 template <int MT>
 __device__ __forceinline__ void lds_wait_first_half(uint4_t (&b)[MT]) {
-  static_assert(MT == 2 || MT == 8, "fragment count");
+  static_assert(MT == 2 || MT == 4 || MT == 8, "fragment count");
   if constexpr (MT == 8) {
     asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+  } else if constexpr (MT == 4) {
+    asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(b[0]), "+v"(b[1]));
   } else {
     asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(b[0]));
   }
 }
 template <int MT>
 __device__ __forceinline__ void lds_wait_rest(uint4_t (&b)[MT]) {
-  static_assert(MT == 2 || MT == 8, "fragment count");
+  static_assert(MT == 2 || MT == 4 || MT == 8, "fragment count");
   if constexpr (MT == 8) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]));
+  } else if constexpr (MT == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[2]), "+v"(b[3]));
   } else {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[1]));
   }

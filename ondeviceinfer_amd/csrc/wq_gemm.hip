@@ -224,12 +224,17 @@ int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, 
 }
 
 // 256-wide n slices when the grid still covers the machine twice over, else
-// 64-wide slices.
+// 64-wide slices.  The narrow form takes 64-row x tiles up to M = 256
+// (32 KiB of LDS, five workgroups per CU): with 128 rows its grids sit just
+// above one round of the 512 resident workgroups (M = 128: fused QKV 40.9 ->
+// 33.3 us, gate_up 94 -> 86 us; the wide form keeps 128 rows, whose weights
+// are then streamed half as often).
 template <GFmt F>
 int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
                      const half_t* bias, half_t* y, hipStream_t s) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128;
   if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
+  if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
   return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
 }
 
