@@ -324,6 +324,29 @@ def test_prefill_gemm_activations_beyond_2gib(gpu, fmt):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize('fmt', ['w4', 'w8'])
+def test_linear_with_k_beyond_gemm_offsets(gpu, fmt):
+    """k = 2^24 + 128 (past the prefill GEMM's 32-bit offsets) at m = 66: W4
+    runs the skinny kernels 64 rows at a time (the 2-row tail included), W8
+    the any-shape kernel; sampled rows against the oracle."""
+    m, k, n = 66, (1 << 24) + 128, 16
+    rows = np.array([0, 1, 63, 64, 65])
+    x = torch.randn(m, k, device=gpu, dtype=torch.float16)
+    xr = host(x[torch.from_numpy(rows).to(gpu)])
+    if fmt == 'w4':
+        name = 'mlp.down_proj.weight'
+        weights, _ = synth.w4_case(n, k, 1, seed=31, name=name)
+        backend, layer = prepared_w4(weights, name, gpu)
+        y = host(backend.linear(x, layer, name))
+        expected = qdq.qdq_linear(xr, weights, name)
+    else:
+        _, q, s, _ = synth.int8_case(n, k, 1, seed=32)
+        y = host(_native.w8a16_linear(x, dev(q, gpu), dev(s, gpu)))
+        expected = int8_ref(xr, q, s)
+    del x
+    check_parity(y[rows], expected, f'{fmt} m={m} k={k} rows')
+
+
 # ------------------------------------------------------------------ INT8 (W8A16)
 
 def int8_ref(x, q, s, bias=None):
