@@ -93,7 +93,7 @@ import torch.nn.functional as F  # noqa: E402
 
 from .attention import cached_scaled_dot_product_attention  # noqa: E402
 from .cache import KVCache, ResidentKVCache  # noqa: E402
-from .functional import rms_norm  # noqa: E402
+from .functional import add_rms_norm, rms_norm  # noqa: E402
 from .layers import RotaryEmbedding, apply_rotary_pos_emb  # noqa: E402
 
 QKV_FUSED = 'self_attn.qkv_proj.weight'
@@ -172,10 +172,8 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
                                                                cache=cache, attention_mask=None, dropout_p=0.0)
     attention_output = attention_output.transpose(1, 2).contiguous().view(batch_size, query_length, hq * d)
     attention_output = linear(attention_output, 'self_attn.o_proj.weight')
-    hidden_states = residual + attention_output
-
-    residual = hidden_states
-    states = rms_norm(hidden_states, weights['post_attention_layernorm.weight'], eps)
+    # residual + attention_output, then the post-attention RMSNorm (one launch on GPU)
+    residual, states = add_rms_norm(residual, attention_output, weights['post_attention_layernorm.weight'], eps)
     if linear_backend is not None and _has_prepared(weights, GATE_UP_FUSED):
         activated = _native.silu_mul(linear(states, GATE_UP_FUSED).contiguous())
     else:

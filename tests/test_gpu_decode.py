@@ -42,6 +42,23 @@ def test_add_rmsnorm(nat, rows, n, with_delta, in_place):
     _close(y.cpu().numpy(), qwen3.rms_norm(s, w, 1e-6))
 
 
+def test_functional_add_rms_norm_equals_two_steps(nat):
+    """The prefill's fused residual add + RMSNorm gives the same bits as torch's
+    fp16 ``+`` followed by ``rms_norm``, and leaves the residual untouched."""
+    from ondeviceinfer_amd.functional import add_rms_norm, rms_norm
+    print('[add_rms_norm] rows=4096 n=5120', flush=True)
+    g = torch.Generator().manual_seed(11)
+    r = (torch.randn(1, 4096, 5120, generator=g) * 3).half().cuda()
+    d = (torch.randn(1, 4096, 5120, generator=g) * 2).half().cuda()
+    w = (1 + 0.1 * torch.randn(5120, generator=g)).half().cuda()
+    r_before = r.clone()
+    summed, normed = add_rms_norm(r, d, w, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(r, r_before)
+    assert torch.equal(summed, r + d)
+    assert torch.equal(normed, rms_norm(r + d, w, 1e-6))
+
+
 def test_silu_mul(nat):
     rng = np.random.default_rng(5)
     gu = (rng.standard_normal((3, 2 * 17408)) * 3).astype(np.float16)
