@@ -68,7 +68,9 @@ int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t kv_heads, 
  *   cos/sin_rows [tokens, 128] fp16 RoPE rows of those positions
  *   key/value_cache [kv_heads, max_seq, 128] fp16; rows start .. start+tokens-1
  *                receive the normalized, rotated k and the v
- *   q_out        [q_heads, tokens, 128] normalized, rotated q
+ *   q_out        [tokens, q_heads, 128] normalized, rotated q (token-major,
+ *                the layout a fused attention reads as [q_heads, tokens, 128]
+ *                strided and writes its output in)
  * Same numerics per element as wq_decode_attention's prologue.  Replaces:
  * the q/k rms_norm + apply_rotary_pos_emb of a multi-token forward
  * (quantized_model.py:177-184, layers.py:64-80) and the cache.update inside

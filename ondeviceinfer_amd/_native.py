@@ -520,7 +520,7 @@ def prefill_qk_rope(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: torc
     """q/k RMSNorm + RoPE of ``tokens`` rows of a fused QKV projection (batch 1)
     at positions ``start ..``; k and v land in rows ``start ..`` of the caches
     (``[kv_heads, max_seq, head_dim]`` fp16); returns q as
-    ``[q_heads, tokens, head_dim]``."""
+    ``[tokens, q_heads, head_dim]`` (token-major)."""
     device = _require_gpu(qkv, q_norm, k_norm, cos_rows, sin_rows, key_cache, value_cache, q_out)
     if key_cache.dim() != 3 or key_cache.shape != value_cache.shape or key_cache.shape[0] != kv_heads:
         raise ValueError(f'caches must be [kv_heads={kv_heads}, max_seq, head_dim], got {tuple(key_cache.shape)}')
@@ -537,9 +537,9 @@ def prefill_qk_rope(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: torc
         if t is not None:
             _check(t, torch.float16, (head_dim,), name)
     if q_out is None:
-        q_out = torch.empty(q_heads, tokens, head_dim, dtype=torch.float16, device=device)
+        q_out = torch.empty(tokens, q_heads, head_dim, dtype=torch.float16, device=device)
     else:
-        _check(q_out, torch.float16, (q_heads, tokens, head_dim), 'q_out')
+        _check(q_out, torch.float16, (tokens, q_heads, head_dim), 'q_out')
     _call('wq_prefill_qk_rope', _ptr(qkv), tokens, q_heads, kv_heads, head_dim, _ptr(q_norm), _ptr(k_norm),
           float(eps), _ptr(cos_rows), _ptr(sin_rows), int(start), _ptr(key_cache), _ptr(value_cache), max_seq,
           _ptr(q_out), _stream(device))

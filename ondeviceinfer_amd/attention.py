@@ -36,3 +36,22 @@ def cached_scaled_dot_product_attention(query: Tensor, key: Tensor, value: Tenso
     return F.scaled_dot_product_attention(query.contiguous(), key.contiguous(), value.contiguous(),
                                           attn_mask=attention_mask, dropout_p=dropout_p, is_causal=is_causal,
                                           enable_gqa=True)
+
+
+def strided_prefill_attention(query: Tensor, key: Tensor, value: Tensor) -> Tensor:
+    """The causal attention of ``cached_scaled_dot_product_attention`` for a
+    resident cache, without its ``.contiguous()`` copies: ``query`` is a
+    ``[batch, q_heads, tokens, d]`` view of token-major memory and ``key`` /
+    ``value`` the attended cache rows ``[batch, kv_heads, end, d]`` read in
+    place.  torch's fused SDPA then returns token-major output, so the
+    decoder's ``transpose(1, 2).contiguous()`` copies nothing; same values as
+    the contiguous form."""
+    query_length, key_length = query.shape[-2], key.shape[-2]
+    attention_mask, is_causal = None, False
+    if query_length > 1:
+        if key_length == query_length:
+            is_causal = True
+        else:
+            attention_mask = build_causal_mask(query_length, key_length, device=query.device)
+    return F.scaled_dot_product_attention(query, key, value, attn_mask=attention_mask, dropout_p=0.0,
+                                          is_causal=is_causal, enable_gqa=True)

@@ -444,7 +444,7 @@ __global__ __launch_bounds__(256) void prefill_qk_rope_kernel(const half_t* __re
   const half2_t c2 = as_h2(reinterpret_cast<const uint32_t*>(cos_t + (size_t)t * kHeadDim)[lane]);
   const half2_t s2 = as_h2(reinterpret_cast<const uint32_t*>(sin_t + (size_t)t * kHeadDim)[lane]);
   const half2_t r = norm_rope_pair(v, nw_p != nullptr, nw, eps, c2, s2, lane);
-  half_t* dst = is_q ? q_out + ((size_t)hh * T + t) * kHeadDim
+  half_t* dst = is_q ? q_out + ((size_t)t * H + hh) * kHeadDim
                      : kc + ((size_t)(hh - H) * max_seq + start + t) * kHeadDim;
   reinterpret_cast<uint32_t*>(dst)[lane] = as_u32(r);
 }

@@ -174,7 +174,8 @@ def test_prefill_qk_rope_matches_oracle(nat, tokens, start, h, kv, with_norm):
         qr, kr = qwen3.rms_norm(qr, qn, eps), qwen3.rms_norm(kr, kn, eps)
     q_ref = qwen3.apply_rope(qr.transpose(1, 0, 2), cos, sin)
     k_ref = qwen3.apply_rope(kr.transpose(1, 0, 2), cos, sin)
-    _close(q.cpu().numpy(), q_ref)
+    assert tuple(q.shape) == (tokens, h, d)
+    _close(q.cpu().numpy().transpose(1, 0, 2), q_ref)
     kcn, vcn = kc.cpu().numpy(), vc.cpu().numpy()
     _close(kcn[:, start:start + tokens], k_ref)
     assert np.array_equal(vcn[:, start:start + tokens], vr.transpose(1, 0, 2))
