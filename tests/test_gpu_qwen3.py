@@ -108,6 +108,22 @@ def test_prefill_then_graph_decode_match_oracle(tiny):
     assert backend.calls - calls == 6 * 4 * TinyCfg.num_hidden_layers
 
 
+def test_chunked_prefill_matches_oracle(tiny):
+    """A prompt in two multi-token chunks: the second chunk attends over cache
+    rows it did not write (the explicit causal mask over the in-place cache
+    rows), every position's logits against the oracle's forward."""
+    np_model, model, _ = tiny
+    cache = model.make_resident_cache(batch_size=1, max_seq_len=160)
+    prompt = np.random.default_rng(2).integers(0, TinyCfg.vocab_size, 100)
+    ocache = qwen3.KVCacheOracle(TinyCfg.num_hidden_layers)
+    for lo, hi in ((0, 61), (61, 100)):
+        print(f'[qwen3] prefill chunk {lo}..{hi}', flush=True)
+        out = model(torch.from_numpy(prompt[lo:hi])[None].cuda(), cache=cache)
+        ref = qwen3.forward(prompt[lo:hi], np_model, TinyCfg, ocache)
+        assert out.logits.shape == (1, hi - lo, TinyCfg.vocab_size) and cache.lengths == [hi, hi]
+        _ok(out.logits[0], ref, f'chunk {lo}..{hi}')
+
+
 def test_graph_decode_equals_eager_decode(tiny):
     np_model, model, _ = tiny
     eager, _ = build(np_model, TinyCfg, decode_graph=False)
