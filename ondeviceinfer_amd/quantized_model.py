@@ -430,8 +430,11 @@ class QuantizedQwen3ForCausalLM:
                 stats=self.compute_stats, linear_backend=self.linear_backend)
             self.runtime.after_layer(layer_idx)
         self.runtime.end_forward()
-        hidden_states = rms_norm(hidden_states, self.final_norm, self.config.rms_norm_eps)
+        # The norm is per row, so keeping the last rows first gives the same
+        # logits as the reference's norm-then-slice without normalizing the
+        # whole prompt.
         if logits_to_keep > 0:
-            hidden_states = hidden_states[:, -logits_to_keep:, :]
+            hidden_states = hidden_states[:, -logits_to_keep:, :].contiguous()
+        hidden_states = rms_norm(hidden_states, self.final_norm, self.config.rms_norm_eps)
         logits = F.linear(hidden_states, self.lm_head)
         return CausalLMOutput(logits=logits, cache=cache)
