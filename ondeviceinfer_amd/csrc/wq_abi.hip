@@ -2,6 +2,7 @@
 #include "wq_common.h"
 #include "wq_status.h"
 
+
 namespace wq {
 
 namespace {
@@ -34,10 +35,15 @@ int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uin
 
 // Largest M served by the MFMA GEMV (4 chunks of 16 activation rows).
 constexpr int64_t kSkinnyMaxM = 64;
-// Largest k of the prefill GEMMs: they address a workgroup's 128 x rows with
-// 32-bit buffer offsets (up to 248 k bytes).  Longer rows run the skinny
-// kernels 64 rows at a time.
-constexpr int64_t kGemmMaxK = 1 << 24;
+// Largest k of the prefill GEMMs.  A workgroup reads its (up to) 128 x rows
+// through one buffer resource whose record count is capped at 2^31 - 1
+// bytes: row r of a 128-k block sits at byte r * 2k + [0, 256), so the last
+// row (127) must stay below that cap, or its reads would come back as zeros.
+// Longer rows run the skinny kernels 64 rows at a time.
+constexpr int64_t kGemmMaxRows = 128;
+constexpr int64_t kGemmMaxK = 1 << 23;
+static_assert((kGemmMaxRows - 1) * 2 * kGemmMaxK + 2 * kW4BlockK <= 0x7fffffff,
+              "GEMM x offsets must fit the 31-bit buffer range");
 
 namespace {
 
@@ -149,3 +155,4 @@ extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const in
                             as_stream(stream));
   return launch_w8_gemm(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
 }
+

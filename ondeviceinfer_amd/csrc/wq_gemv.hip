@@ -14,8 +14,6 @@
 #include "wq_common.h"
 #include "wq_status.h"
 
-#include <stdlib.h>
-
 namespace wq {
 namespace {
 
@@ -699,11 +697,6 @@ struct FlatPlan {
   int split, ksw;
 };
 
-int env_int(const char* name) {
-  const char* e = getenv(name);
-  return e ? atoi(e) : 0;
-}
-
 // Work split for the flat GEMV, from sweeps of the Qwen3-14B shapes on
 // MI355X.  Long-K, short-N shapes (17408 -> 5120: 320 tiles x 136 blocks)
 // split each tile's k range over four 4-wave workgroups, so the 1280
@@ -711,18 +704,14 @@ int env_int(const char* name) {
 // same share; one 12-wave workgroup per tile fits only once per CU at that
 // register count and leaves a second launch wave.  Otherwise one workgroup
 // per tile: 12 waves for N < 1024 tiles (enough loads in flight), 4 for wide
-// N.  WQ_GEMV_SPLIT / WQ_GEMV_KSW override it in tuning runs.
+// N.
 template <WFmt F>
 FlatPlan plan_flat(int ntile, int nblk, bool may_split = true) {
   FlatPlan p{1, 1};
   if (ntile < 512 && nblk >= 64) p.split = 4;
-  const int fs = env_int("WQ_GEMV_SPLIT");
-  if (fs == 1 || fs == 2 || fs == 4 || fs == 8) p.split = fs;
   if (p.split > nblk || !may_split) p.split = 1;
   const int per = nblk / p.split;
   int ksw = p.split > 1 || ntile >= 1024 ? 4 : 12;
-  const int fk = env_int("WQ_GEMV_KSW");
-  if (fk >= 1 && fk <= 16) ksw = fk;
   if (ksw > per) ksw = per;
   if (ksw < 1) ksw = 1;
   const int limit = per / ksw <= (F == WFmt::W4 ? 12 : 8) ? 16 : 8;

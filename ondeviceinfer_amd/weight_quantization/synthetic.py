@@ -2,13 +2,15 @@
 
 There is no real checkpoint or network on the benchmark machines, so the
 end-to-end benchmark and the loader tests need pack-quantized weights of the
-right shapes.  ``random_compressed_store`` draws them directly in the
-compressed-tensors layout that ``load_compressed_store`` validates
+right shapes.  ``random_compressed_store`` draws each decoder linear as fp16
+``N(0, 0.02)`` and quantizes it (``awq_quantize``: asymmetric uint4, min-max
+round-to-nearest per row and group along K, the range widened to include 0)
+into the compressed-tensors layout that ``load_compressed_store`` validates
 (``ondeviceinfer/weight_quantization/backend.py:69-128``): per linear
-``weight_packed`` int32 ``[n, k/8]`` (random codes), ``weight_scale`` fp16
-``[n, k/G]`` (positive), ``weight_zero_point`` int32 ``[n/8, k/G]`` (random
-codes; omitted for symmetric uint4b8), ``weight_shape``; fp16 norms near 1;
-fp16 embedding and LM head on the host, as the reference keeps them.
+``weight_packed`` int32 ``[n, k/8]``, ``weight_scale`` fp16 ``[n, k/G]``,
+``weight_zero_point`` int32 ``[n/8, k/G]`` (omitted for symmetric uint4b8),
+``weight_shape``; fp16 norms near 1; fp16 embedding and LM head on the host,
+as the reference keeps them.
 
 ``write_compressed_checkpoint`` writes such a store as safetensors shards +
 ``model.safetensors.index.json`` + ``config.json`` with a
@@ -41,28 +43,65 @@ def linear_shapes(cfg: Qwen3Config) -> dict[str, tuple[int, int]]:
     }
 
 
+def pack_nibbles(codes: torch.Tensor, axis: int) -> torch.Tensor:
+    """uint4 codes (int32 in [0, 15]) -> int32 words of 8 codes, first code in
+    the lowest bits: along K (``axis=1``, ``[n, k] -> [n, k/8]``) or along N
+    (``axis=0``, ``[n, g] -> [n/8, g]``), the compressed-tensors packing."""
+    if axis == 0:
+        return pack_nibbles(codes.t(), 1).t().contiguous()
+    rows, cols = codes.shape
+    shifts = torch.arange(0, 32, 4, device=codes.device, dtype=torch.int64)
+    words = (codes.reshape(rows, cols // 8, 8).to(torch.int64) << shifts).sum(-1)
+    return (words - ((words >> 31) << 32)).to(torch.int32)   # two's complement of the 32-bit pattern
+
+
+def awq_quantize(w: torch.Tensor, group_size: int = 128, *, symmetric: bool = False) -> dict[str, torch.Tensor]:
+    """fp16 ``w [n, k]`` -> unprefixed pack-quantized tensors, in fp32 on
+    ``w``'s device.  Asymmetric: per (row, group) ``s = fp16((max - min) / 15)``
+    over the group's range widened to include 0, ``z = clamp(round(-min / s),
+    0, 15)``, ``q = clamp(round(w / s) + z, 0, 15)``.  Symmetric (uint4b8):
+    ``s = fp16(absmax / 7.5)``, ``q = clamp(round(w / s) + 8, 0, 15)``.  A zero
+    range gives ``s = 1``; rounding is half-to-even."""
+    n, k = w.shape
+    if k % group_size or n % 8:
+        raise ValueError('need k % group_size == 0 and n % 8 == 0')
+    g = w.float().reshape(n, k // group_size, group_size)
+    if symmetric:
+        s16 = (g.abs().amax(-1) / 7.5).half()
+        s16 = torch.where(s16 == 0, torch.ones_like(s16), s16)
+        q = torch.clamp(torch.round(g / s16.float()[..., None]) + 8, 0, 15).to(torch.int32).reshape(n, k)
+        return {'weight_packed': pack_nibbles(q, 1), 'weight_scale': s16,
+                'weight_shape': torch.tensor([n, k], dtype=torch.int64)}
+    lo = torch.clamp(g.amin(-1), max=0.0)
+    hi = torch.clamp(g.amax(-1), min=0.0)
+    s16 = ((hi - lo) / 15.0).half()
+    s16 = torch.where(s16 == 0, torch.ones_like(s16), s16)
+    s = s16.float()
+    z = torch.clamp(torch.round(-lo / s), 0, 15)
+    q = torch.clamp(torch.round(g / s[..., None]) + z[..., None], 0, 15).to(torch.int32).reshape(n, k)
+    return {'weight_packed': pack_nibbles(q, 1), 'weight_scale': s16,
+            'weight_zero_point': pack_nibbles(z.to(torch.int32), 0),
+            'weight_shape': torch.tensor([n, k], dtype=torch.int64)}
+
+
 def random_compressed_store(cfg: Qwen3Config, *, seed: int = 0, device: str | torch.device = 'cpu',
-                            group_size: int = 128, symmetric: bool = False,
-                            scale_range: tuple[float, float] = (0.0005, 0.0025)) -> CompressedStore:
-    """A random W4 (G=``group_size``) Qwen3 model; decoder tensors on ``device``,
-    embedding / final norm / LM head on the host."""
+                            group_size: int = 128, symmetric: bool = False, std: float = 0.02) -> CompressedStore:
+    """A random W4 (G=``group_size``) Qwen3 model: every decoder linear drawn
+    as ``fp16(N(0, std))`` and quantized by :func:`awq_quantize` on ``device``,
+    where the decoder tensors stay; embedding / final norm / LM head
+    (``fp16(N(0, 0.02))``, norms near 1) on the host."""
     device = torch.device(device)
     gen = torch.Generator(device=device).manual_seed(seed)
     cpu_gen = torch.Generator().manual_seed(seed + 1)
-    lo, hi = scale_range
     layers = []
     for _ in range(cfg.num_hidden_layers):
         layer = {}
         for name, (n, k) in linear_shapes(cfg).items():
             prefix = name.removesuffix('.weight')
-            layer[prefix + '.weight_packed'] = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32,
-                                                             device=device, generator=gen)
-            layer[prefix + '.weight_scale'] = (torch.rand((n, k // group_size), device=device, generator=gen)
-                                               * (hi - lo) + lo).half()
-            if not symmetric:
-                layer[prefix + '.weight_zero_point'] = torch.randint(-2**31, 2**31 - 1, (n // 8, k // group_size),
-                                                                     dtype=torch.int32, device=device, generator=gen)
-            layer[prefix + '.weight_shape'] = torch.tensor([n, k], dtype=torch.int64)
+            w = (torch.randn((n, k), device=device, generator=gen) * std).half()
+            for key, value in awq_quantize(w, group_size, symmetric=symmetric).items():
+                layer[f'{prefix}.{key}'] = value
+            del w
         for name in NORM_WEIGHT_NAMES:
             size = cfg.head_dim if 'q_norm' in name or 'k_norm' in name else cfg.hidden_size
             layer[name] = (1.0 + 0.1 * torch.randn(size, device=device, generator=gen)).half()
@@ -73,7 +112,8 @@ def random_compressed_store(cfg: Qwen3Config, *, seed: int = 0, device: str | to
     lm_head = embed if cfg.tie_word_embeddings else \
         (torch.randn(cfg.vocab_size, cfg.hidden_size, device=device, generator=big) * 0.02).half().cpu()
     final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden_size, generator=cpu_gen)).half()
-    manifest = {'source': 'synthetic', 'seed': seed, 'quantization_config': quantization_config(group_size, symmetric)}
+    manifest = {'source': 'synthetic', 'seed': seed, 'weight_std': std,
+                'quantization_config': quantization_config(group_size, symmetric)}
     return CompressedStore(cfg, layers, embed, final_norm, lm_head, manifest)
 
 
@@ -131,5 +171,5 @@ def write_compressed_checkpoint(path: str | Path, store: CompressedStore, *, lay
     return path
 
 
-__all__ = ['linear_shapes', 'random_compressed_store', 'quantization_config', 'write_compressed_checkpoint',
+__all__ = ['awq_quantize', 'linear_shapes', 'pack_nibbles', 'random_compressed_store', 'quantization_config', 'write_compressed_checkpoint',
            'LINEAR_WEIGHT_NAMES']

@@ -102,7 +102,7 @@ def decode_weight(weights: dict, name: str, *, group_size: int = 128) -> np.ndar
         scale = np.asarray(weights[prefix + '.weight_scale'])
         return (q.astype(np.float32) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float16)
     n, k = (int(x) for x in np.asarray(weights[prefix + '.weight_shape']).tolist())
-    q = unpack_unsigned(weights[prefix + '.weight_packed'], 4, 1, k)
+    packed = np.asarray(weights[prefix + '.weight_packed'])
     scale = np.asarray(weights[prefix + '.weight_scale']).astype(np.float32)
     zero = weights.get(prefix + '.weight_zero_point')
     if zero is None:
@@ -114,7 +114,30 @@ def decode_weight(weights: dict, name: str, *, group_size: int = 128) -> np.ndar
         groups = np.asarray(g_idx).astype(np.int64)
     else:
         groups = np.arange(k) // group_size
-    return ((q.astype(np.float32) - zero[:, groups].astype(np.float32)) * scale[:, groups]).astype(np.float16)
+    out = np.empty((n, k), dtype=np.float16)
+
+    def rows(r0: int, r1: int) -> None:
+        # Every row decodes independently; blocks of rows keep the
+        # temporaries small, and numpy runs the blocks on several threads.
+        q = unpack_unsigned(packed[r0:r1], 4, 1, k).astype(np.float32)
+        out[r0:r1] = (q - zero[r0:r1][:, groups].astype(np.float32)) * scale[r0:r1][:, groups]
+
+    _row_blocks(n, k, rows)
+    return out
+
+
+def _row_blocks(n: int, k: int, fn) -> None:
+    """Run ``fn(r0, r1)`` over row blocks of about 2M elements, on a thread
+    pool when there is more than one block."""
+    step = max(8, (1 << 21) // max(k, 1) // 8 * 8)
+    blocks = [(r0, min(n, r0 + step)) for r0 in range(0, n, step)]
+    if len(blocks) == 1:
+        fn(*blocks[0])
+        return
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=min(len(blocks), os.cpu_count() or 1, 16)) as pool:
+        list(pool.map(lambda b: fn(*b), blocks))
 
 
 def decode_rows(weights: dict, name: str, rows: np.ndarray) -> np.ndarray:
@@ -201,13 +224,30 @@ def linear_fp32(x: np.ndarray, weight_fp16: np.ndarray, bias: np.ndarray | None 
     ``quantization.py:353``, ``quantized_model.py:121``); the accumulation type
     is fixed to fp32 as the parity contract states.  ``x [..., K]``, ``W [N, K]``.
     """
+    return _linear_w32(x, np.asarray(weight_fp16).astype(np.float32), bias)
+
+
+def _linear_w32(x: np.ndarray, w32: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
     x32 = np.asarray(x).astype(np.float32)
-    w32 = np.asarray(weight_fp16).astype(np.float32)
     lead = x32.shape[:-1]
     y = x32.reshape(-1, x32.shape[-1]) @ w32.T
     if bias is not None:
         y = y + np.asarray(bias).astype(np.float32)
     return y.astype(np.float16).reshape(*lead, w32.shape[0])
+
+
+class DecodedLinear:
+    """``qdq_linear`` (or ``linear_fp32`` of an fp16 weight) with the decode
+    and the fp32 widening of the weight done once, for repeated calls at
+    model scale: every call returns exactly what ``qdq_linear`` would."""
+
+    def __init__(self, weights: dict | None, name: str | None = None, *, group_size: int = 128,
+                 weight_fp16: np.ndarray | None = None):
+        w16 = weight_fp16 if weights is None else decode_weight(weights, name, group_size=group_size)
+        self.w32 = np.asarray(w16).astype(np.float32)
+
+    def __call__(self, x: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+        return _linear_w32(x, self.w32, bias)
 
 
 def qdq_linear(x: np.ndarray, weights: dict, name: str, *, group_size: int = 128) -> np.ndarray:

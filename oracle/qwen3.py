@@ -179,16 +179,25 @@ def forward(token_ids: np.ndarray, model: dict, cfg, cache: KVCacheOracle | None
     ``QuantizedQwen3ForCausalLM.__call__`` (``quantized_model.py:280-338``):
     embedding, layers at positions ``past .. past + S - 1``, final norm, fp16
     LM head.  ``model``: ``embed_tokens``, ``layers`` (list of weight dicts),
-    ``final_norm``, ``lm_head``."""
+    ``final_norm``, ``lm_head``; optionally ``linears`` (per layer, a dict of
+    weight name -> ``qdq.DecodedLinear``) and ``lm_head_linear``, which give
+    the same results with each weight decoded once."""
     ids = np.asarray(token_ids).reshape(-1)
     hidden = np.asarray(model['embed_tokens'])[ids].astype(F16)
     past = cache.length(0) if cache is not None else 0
     cos, sin = rotary_tables(cfg.head_dim, cfg.rope_theta, np.arange(past, past + ids.size))
+    decoded = model.get('linears')
     for idx, weights in enumerate(model['layers']):
-        hidden = decoder_layer(hidden, weights, cfg, idx, cos, sin, cache)
+        linear = None
+        if decoded is not None:
+            def linear(x, name, _d=decoded[idx]):
+                return _d[name](x)
+        hidden = decoder_layer(hidden, weights, cfg, idx, cos, sin, cache, linear=linear)
     hidden = rms_norm(hidden, model['final_norm'], cfg.rms_norm_eps)
     if logits_to_keep > 0:
         hidden = hidden[-logits_to_keep:]
+    if model.get('lm_head_linear') is not None:
+        return model['lm_head_linear'](hidden)
     return qdq.linear_fp32(hidden, model['lm_head'])
 
 

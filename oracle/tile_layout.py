@@ -25,11 +25,8 @@ then the two zero-point words of those rows, copied from
 ``weight_zero_point[2t, g]`` and ``[2t+1, g]`` (``0x88888888`` = z 8 for the
 symmetric uint4b8 format).
 
-W8 layout (K a multiple of 64)
-------------------------------
-``tiles``: int8 ``[N16/16, K/64, 64, 16]``; lane ``l`` owns row ``16t + l%16``,
-k ``64*blk + 16*(l//16) + [0, 16)`` in natural order.  ``meta``: fp16 per-row
-scale ``[N16]``, zero-padded.
+INT8 weights have no tile layout: the kernels read them in their stored
+row-major ``[N, K]`` form.
 """
 from __future__ import annotations
 
@@ -37,7 +34,6 @@ import numpy as np
 
 NIBBLE_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)   # nibble p holds element NIBBLE_ORDER[p]
 W4_BLOCK_K = 128
-W8_BLOCK_K = 64
 W4_META_BYTES = 40
 SYMMETRIC_ZERO_WORD = 0x88888888
 
@@ -114,28 +110,3 @@ def w4_dequant(tiles: np.ndarray, meta: np.ndarray, n: int, k: int, group_size: 
     z = unpack_unsigned(zero, 4, 0, n).astype(np.float32)
     groups = np.arange(k) // group_size
     return ((q - z[:, groups]) * scale.astype(np.float32)[:, groups]).astype(np.float16)
-
-
-def w8_check(n: int, k: int) -> None:
-    if n <= 0 or k <= 0 or k % W8_BLOCK_K:
-        raise ValueError('W8 tile layout needs K % 64 == 0')
-
-
-def w8_repack(qweight: np.ndarray, scale: np.ndarray, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:
-    w8_check(n, k)
-    n16 = _ceil16(n)
-    q = np.zeros((n16, k), dtype=np.int8)
-    q[:n] = np.asarray(qweight).reshape(n, k)
-    tiles = q.reshape(n16 // 16, 16, k // W8_BLOCK_K, 4, 16).transpose(0, 2, 3, 1, 4).reshape(
-        n16 // 16, k // W8_BLOCK_K, 64, 16).copy()
-    meta = np.zeros(n16, dtype=np.float16)
-    meta[:n] = np.asarray(scale).astype(np.float16).reshape(n)
-    return tiles, meta
-
-
-def w8_unpack(tiles: np.ndarray, meta: np.ndarray, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:
-    w8_check(n, k)
-    n16 = _ceil16(n)
-    t = np.asarray(tiles).view(np.int8).reshape(n16 // 16, k // W8_BLOCK_K, 4, 16, 16)
-    q = t.transpose(0, 3, 1, 2, 4).reshape(n16, k)
-    return q[:n].copy(), np.asarray(meta).view(np.float16)[:n].copy()

@@ -125,17 +125,17 @@ def test_w4a16_skinny_four_tiles_per_wave(gpu, m):
     check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 skinny m={m} n=16400')
 
 
-@pytest.mark.parametrize('ksw,split', [('1', '1'), ('3', '1'), ('16', '1'), ('3', '2'), ('2', '4')])
-def test_w4a16_decode_wave_split_override(gpu, monkeypatch, ksw, split):
-    """Uneven block counts per wave and per k-split (tuning overrides)."""
-    monkeypatch.setenv('WQ_GEMV_KSW', ksw)
-    monkeypatch.setenv('WQ_GEMV_SPLIT', split)
+@pytest.mark.parametrize('n,k', [(1000, 128), (1000, 384), (1000, 5248), (1000, 8448), (16400, 640)])
+def test_w4a16_decode_uneven_wave_splits(gpu, n, k):
+    """Decode plans with uneven work: one block (one wave), 3 blocks over 3
+    waves, 41 blocks over 12 waves (5 waves take an extra block), 66 blocks
+    over 4 k-splits of 16 / 17 blocks, and 5 blocks over 4 waves on a wide N."""
     name = 'p.weight'
     for m in (1, 3):
-        weights, x = synth.w4_case(1000, 1024, m, seed=int(ksw) + m, name=name)
+        weights, x = synth.w4_case(n, k, m, seed=k + m, name=name)
         backend, layer = prepared_w4(weights, name, gpu)
         y = backend.linear(dev(x, gpu), layer, name)
-        check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 ksw={ksw} split={split} m={m}')
+        check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 n={n} k={k} m={m}')
 
 
 def test_w4a16_group_256_and_symmetric(gpu):
@@ -325,8 +325,34 @@ def test_prefill_gemm_activations_beyond_2gib(gpu, fmt):
 
 
 @pytest.mark.parametrize('fmt', ['w4', 'w8'])
+@pytest.mark.parametrize('k', [1 << 23, (1 << 23) + 128])
+def test_prefill_gemm_at_the_largest_k(gpu, fmt, k):
+    """k = 2^23, the largest the prefill GEMM takes (row 127 of a 128-row x tile
+    then sits just under the 2^31-byte buffer range), and one block more, which
+    goes to the skinny / any-shape kernels; m = 300 selects the 128-row tiles.
+    Sampled rows include rows 64..127 of a tile, the ones a too-small range
+    would read as zeros."""
+    m, n = 300, 16
+    rows = np.array([0, 63, 64, 100, 127, 128, 191, 192, 255, 256, 299])
+    x = torch.randn(m, k, device=gpu, dtype=torch.float16)
+    xr = host(x[torch.from_numpy(rows).to(gpu)])
+    if fmt == 'w4':
+        name = 'mlp.down_proj.weight'
+        weights, _ = synth.w4_case(n, k, 1, seed=41, name=name)
+        backend, layer = prepared_w4(weights, name, gpu)
+        y = host(backend.linear(x, layer, name))
+        expected = qdq.qdq_linear(xr, weights, name)
+    else:
+        _, q, s, _ = synth.int8_case(n, k, 1, seed=42)
+        y = host(_native.w8a16_linear(x, dev(q, gpu), dev(s, gpu)))
+        expected = int8_ref(xr, q, s)
+    del x
+    check_parity(y[rows], expected, f'{fmt} m={m} k={k} rows')
+
+
+@pytest.mark.parametrize('fmt', ['w4', 'w8'])
 def test_linear_with_k_beyond_gemm_offsets(gpu, fmt):
-    """k = 2^24 + 128 (past the prefill GEMM's 32-bit offsets) at m = 66: W4
+    """k = 2^24 + 128 (past the prefill GEMM's largest k) at m = 66: W4
     runs the skinny kernels 64 rows at a time (the 2-row tail included), W8
     the any-shape kernel; sampled rows against the oracle."""
     m, k, n = 66, (1 << 24) + 128, 16

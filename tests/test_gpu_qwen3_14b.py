@@ -1,0 +1,164 @@
+"""configs[4] at its real geometry: Qwen3-14B-shaped W4A16 decoders (hidden
+5120, 40 / 8 heads of 128, SwiGLU 17408, vocab 151936) on the GPU.
+
+* Two layers against the oracle's forward (oracle/qwen3.py with the QDQ
+  linears, each weight decoded once): a 512-token prefill through the fused
+  QKV GEMM, ``prefill_qk_rope`` and attention over the in-place cache rows,
+  then graph-replayed decode steps (fused RMSNorm / SiLU*up / residual GEMVs,
+  decode attention, LM head with the greedy token).
+* The full 40-layer model with a 4096-token prompt (the benchmark's workload):
+  8 graph-replayed decode steps against the eager path (per-layer torch ops,
+  the unfused linears and SDPA over the cache) on a second cache holding the
+  same prompt: finite logits, graph logits within a bar calibrated by the
+  rounding noise between two correct paths, the in-graph greedy token equal
+  to argmax of the graph's logits, and equal to the eager argmax wherever the
+  eager top-2 gap exceeds twice the largest graph-eager logit difference.
+
+Weights are ``fp16(N(0, 0.02))`` quantized to uint4 G=128.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qdq, qwen3
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg(layers):
+    from ondeviceinfer_amd.config import QWEN3_14B, Qwen3Config
+    return Qwen3Config.from_dict(dict(QWEN3_14B, num_hidden_layers=layers))
+
+
+def _model(cfg, gpu):
+    from ondeviceinfer_amd.quantized_model import QuantizedQwen3ForCausalLM
+    from ondeviceinfer_amd.weight_quantization.backend import CompressedLinearBackend, CompressedResidentRuntime
+    from ondeviceinfer_amd.weight_quantization.synthetic import random_compressed_store
+    store = random_compressed_store(cfg, seed=0, device=gpu)
+    backend = CompressedLinearBackend('marlin')
+    runtime = CompressedResidentRuntime(store, backend, device=gpu, verbose=False)
+    model = QuantizedQwen3ForCausalLM(store, runtime, device=gpu, linear_backend=backend)
+    torch.cuda.synchronize()
+    return store, model, backend
+
+
+def _oracle_model(store):
+    """numpy copies of the store, each linear decoded once (qdq.DecodedLinear)."""
+    layers, linears = [], []
+    for layer in store.layers:
+        np_layer = {k: v.cpu().numpy() for k, v in layer.items()}
+        layers.append(np_layer)
+        linears.append({name: qdq.DecodedLinear(np_layer, name) for name in qwen3.LINEAR_NAMES})
+    lm_head = store.lm_head.cpu().numpy()
+    return {'layers': layers, 'linears': linears, 'embed_tokens': store.embed_tokens.cpu().numpy(),
+            'final_norm': store.final_norm.cpu().numpy(), 'lm_head': lm_head,
+            'lm_head_linear': qdq.DecodedLinear(None, weight_fp16=lm_head)}
+
+
+def _parity(got, ref, what):
+    m = qdq.parity_metrics(np.asarray(got, dtype=np.float32), np.asarray(ref, dtype=np.float32))
+    print(what, {k: (round(v, 8) if isinstance(v, float) else v) for k, v in m.items()}, flush=True)
+    assert qdq.parity_ok(m), (what, m)
+
+
+def test_two_layers_at_14b_geometry_match_oracle(gpu):
+    cfg = _cfg(2)
+    print('[14b-2l] building the model', flush=True)
+    store, model, backend = _model(cfg, gpu)
+    oracle_model = _oracle_model(store)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, 512)
+    cache = model.make_resident_cache(batch_size=1, max_seq_len=600)
+    assert cache._decode_graph is not None
+    ocache = qwen3.KVCacheOracle(cfg.num_hidden_layers)
+    print('[14b-2l] prefill 512 tokens', flush=True)
+    out = model(torch.from_numpy(prompt)[None].to(gpu), cache=cache, logits_to_keep=1)
+    ref = qwen3.forward(prompt, oracle_model, cfg, ocache, logits_to_keep=1)
+    assert out.logits.shape == (1, 1, cfg.vocab_size) and cache.lengths == [512, 512]
+    _parity(out.logits[0].float().cpu().numpy(), ref, 'prefill 512')
+    token = out.logits[:, -1].argmax(-1, keepdim=True)
+    calls = backend.calls
+    for step in range(5):
+        print(f'[14b-2l] decode step {step}', flush=True)
+        out = model(token, cache=cache, logits_to_keep=1)
+        assert out.next_token is not None      # the decode graph ran
+        ref = qwen3.forward(token.cpu().numpy().reshape(-1), oracle_model, cfg, ocache, logits_to_keep=1)
+        _parity(out.logits[0].float().cpu().numpy(), ref, f'decode {step}')
+        assert torch.equal(out.next_token, out.logits[:, -1].argmax(-1, keepdim=True))
+        token = out.next_token
+    assert cache.lengths == [517, 517]
+    assert backend.calls - calls == 5 * 4 * cfg.num_hidden_layers
+    # The K/V rows the decode graph appended, against the oracle's cache.
+    for layer in range(cfg.num_hidden_layers):
+        _parity(cache.key_cache[layer][0, :, :517].float().cpu().numpy(), ocache.k[layer], f'K cache layer {layer}')
+        _parity(cache.value_cache[layer][0, :, :517].float().cpu().numpy(), ocache.v[layer],
+                f'V cache layer {layer}')
+
+
+def test_forty_layers_4096_prompt_graph_against_eager(gpu):
+    """Graph decode against the eager path at 40 layers.  Two fp16
+    implementations of a 40-layer network drift apart by rounding alone, so
+    the bar is calibrated in the same run: a third path, eager with the
+    explicit-QDQ backend (``reference_int4``: fp16 decode + torch's GEMM), sets
+    the rounding-noise floor between two correct implementations, and graph
+    vs eager must stay within twice that floor (and within the Linear bar of
+    the 2-layer test wherever the floor is lower)."""
+    from ondeviceinfer_amd.quantized_model import QuantizedQwen3ForCausalLM
+    from ondeviceinfer_amd.weight_quantization.backend import CompressedLinearBackend, CompressedResidentRuntime
+    cfg = _cfg(40)
+    print('[14b-40l] building the model', flush=True)
+    store, model, _ = _model(cfg, gpu)
+    ref_backend = CompressedLinearBackend('reference_int4')
+    ref_model = QuantizedQwen3ForCausalLM(store, CompressedResidentRuntime(store, ref_backend, device=gpu,
+                                                                           verbose=False),
+                                          device=gpu, linear_backend=ref_backend, decode_graph=False)
+    prompt = torch.randint(0, cfg.vocab_size, (1, 4096), generator=torch.Generator().manual_seed(0)).to(gpu)
+    graph_cache = model.make_resident_cache(batch_size=1, max_seq_len=4112)
+    eager_cache = model.make_resident_cache(batch_size=1, max_seq_len=4112)
+    ref_cache = ref_model.make_resident_cache(batch_size=1, max_seq_len=4112)
+    assert graph_cache._decode_graph is not None and ref_cache._decode_graph is None
+    print('[14b-40l] prefill 4096 tokens on three caches', flush=True)
+    first = model(prompt, cache=graph_cache, logits_to_keep=1).logits
+    again = model(prompt, cache=eager_cache, logits_to_keep=1).logits
+    ref_first = ref_model(prompt, cache=ref_cache, logits_to_keep=1).logits
+    assert torch.isfinite(first).all() and torch.isfinite(ref_first).all()
+    print(f'[14b-40l] prefill logits bit-identical across two caches: {torch.equal(first, again)}', flush=True)
+    _parity(again[0, -1].float().cpu().numpy(), first[0, -1].float().cpu().numpy(), 'prefill twice')
+    token = first[:, -1].argmax(-1, keepdim=True)
+    decisive = 0
+    for step in range(8):
+        pos = torch.tensor([[4096 + step]], device=gpu)
+        g_out = model(token, cache=graph_cache, logits_to_keep=1)
+        assert g_out.next_token is not None
+        e_out = model(token, cache=eager_cache, position_ids=pos, logits_to_keep=1)
+        r_out = ref_model(token, cache=ref_cache, position_ids=pos, logits_to_keep=1)
+        g, e, r = (o.logits[0, -1].float().cpu().numpy() for o in (g_out, e_out, r_out))
+        assert np.isfinite(g).all() and np.isfinite(e).all() and np.isfinite(r).all()
+        floor = qdq.parity_metrics(e, r)
+        got = qdq.parity_metrics(g, e)
+        print(f'[14b-40l] step {step}: graph vs eager {got}; noise floor (eager vs explicit QDQ) {floor}',
+              flush=True)
+        assert got['cosine'] >= 0.9999 and floor['cosine'] >= 0.9999
+        assert got['mean_rel'] <= max(2e-3, 2 * floor['mean_rel'])
+        assert got['max_abs'] <= max(1e-2 * got['ref_inf'], 2 * floor['max_abs'])
+        g_tok = int(g_out.next_token.item())
+        assert g_tok == int(np.argmax(g))      # the in-graph pick is argmax's rule on the same logits
+        top2 = np.sort(e)[-2:]
+        if top2[1] - top2[0] > 2 * float(np.abs(g - e).max()):
+            assert g_tok == int(np.argmax(e)), f'step {step}'
+            decisive += 1
+        print(f'[14b-40l] step {step}: token {g_tok}, eager top-2 gap {top2[1] - top2[0]:.4f}, '
+              f'max |graph - eager| {np.abs(g - e).max():.4f}', flush=True)
+        token = g_out.next_token
+    print(f'[14b-40l] decisive steps: {decisive} of 8', flush=True)
+    assert graph_cache.lengths == eager_cache.lengths == [4104] * 40
+    # The K/V rows of the 8 decode positions written by the graph and by the
+    # eager path, at the first, middle and last layer, against the same noise
+    # floor (the explicit-QDQ path's rows).
+    for layer in (0, 19, 39):
+        for name, caches in (('K', (graph_cache.key_cache, eager_cache.key_cache, ref_cache.key_cache)),
+                             ('V', (graph_cache.value_cache, eager_cache.value_cache, ref_cache.value_cache))):
+            g, e, r = (c[layer][0, :, 4096:4104].float().cpu().numpy() for c in caches)
+            got, floor = qdq.parity_metrics(g, e), qdq.parity_metrics(e, r)
+            print(f'[14b-40l] {name} rows layer {layer}: graph vs eager {got}; floor {floor}', flush=True)
+            assert got['cosine'] >= 0.9999
+            assert got['mean_rel'] <= max(2e-3, 2 * floor['mean_rel'])

@@ -220,17 +220,6 @@ def test_w4_tile_round_trip_and_dequant(n, k, g, sym):
                           qdq.decode_weight(weights, 'p.weight', group_size=g).view(np.uint16))
 
 
-def test_w8_tile_round_trip():
-    rng = np.random.default_rng(6)
-    q = rng.integers(-127, 128, size=(40, 256)).astype(np.int8)
-    s = (rng.random(40) + 0.1).astype(np.float16)
-    tiles, meta = tile_layout.w8_repack(q, s, 40, 256)
-    q2, s2 = tile_layout.w8_unpack(tiles, meta, 40, 256)
-    assert np.array_equal(q2, q) and np.array_equal(s2, s)
-
-
-# --------------------------------------------------------------------------- synthetic inputs
-
 def test_awq_synthetic_quantizer_is_valid_and_close():
     n, k = 32, 512
     rng = np.random.default_rng(0)
