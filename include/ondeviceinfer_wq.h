@@ -103,6 +103,22 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
                     int64_t n, int64_t group_size, uint16_t* y,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* wq_w4a16_linear without a workspace argument and without any allocation:
+ * the decode GEMV's k-split counters and partials live in a fixed 4 MiB
+ * device array inside the library (one per GPU, held until the process
+ * ends), so the call is as fast as wq_w4a16_linear with its workspace.
+ * Every call on a GPU shares that GPU's array: calls that may overlap on one
+ * GPU (different streams, or graphs replayed concurrently) race and must be
+ * ordered by the caller.  The first call on a device looks the array up
+ * (hipGetSymbolAddress) and queues a clear of it on `stream`.  Shapes whose
+ * split plan would need more than 4 MiB return WQ_ERR_WORKSPACE (none of the
+ * planner's current shapes do: its largest split needs 2 MiB).
+ * No counterpart in the reference: it exists for callers that cannot
+ * allocate (code under HIP graph capture, serving loops and harnesses that
+ * forbid hipMalloc). */
+int wq_w4a16_linear_noalloc(const uint16_t* x, int64_t m, int64_t k, const void* tiles, const void* meta,
+                            int64_t n, int64_t group_size, uint16_t* y, void* stream);
+
 /* One decode-token (M = 1) W4A16 linear with the neighbouring elementwise
  * work of the Qwen3 decoder layer folded in (n % 16 == 0):
  *   x_mode 0  x as given ([k]);

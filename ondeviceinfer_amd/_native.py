@@ -48,6 +48,7 @@ _SIGNATURES = {
     'wq_w4_decode': [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P],
     'wq_w4a16_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
     'wq_w4a16_linear': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, ctypes.c_size_t, _P],
+    'wq_w4a16_linear_noalloc': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P],
     'wq_w4a16_decode_fused': [_P, _I64, _P, _P, _I64, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P,
                               _P, _P, ctypes.c_size_t, _P],
     'wq_w8_decode': [_P, _P, _I64, _I64, _P, _P],

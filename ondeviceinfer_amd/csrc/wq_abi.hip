@@ -2,6 +2,7 @@
 #include "wq_common.h"
 #include "wq_status.h"
 
+#include <mutex>
 
 namespace wq {
 
@@ -156,3 +157,78 @@ extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const in
   return launch_w8_gemm(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free W4A16 linear (wq_w4a16_linear_noalloc).
+//
+// The decode GEMV's k-split counters and fp32 partials live in this
+// file-scope device array instead of a caller workspace.  Each GPU holds its
+// own copy for the life of the process.  Host code never passes `scratch`
+// itself to a kernel: the name is only a host-side handle, so every use
+// goes through the device address that hipGetSymbolAddress returns for the
+// current device, kept in g_scratch_ptr.  The largest split plan (511 tiles x
+// 4 splits x 1 KiB plus 2 KiB of counters) needs 2.0 MiB.
+namespace wq {
+constexpr size_t kNoAllocScratchBytes = 4u << 20;
+}  // namespace wq
+
+static __device__ __align__(256) uint8_t scratch[wq::kNoAllocScratchBytes];
+
+namespace wq {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint4_t* p, size_t n16) {
+  for (size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x; j < n16; j += (size_t)gridDim.x * blockDim.x)
+    p[j] = uint4_t{0u, 0u, 0u, 0u};
+}
+
+// Device address of `scratch` on the current device.  The first call on a
+// device looks the address up and queues a clear of the whole array on
+// `stream` (the split counters must start at zero; every later call leaves
+// them at zero again), ahead of the caller's kernels on that stream.
+int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("hipGetDevice failed: %s", hipGetErrorString(e));
+    return WQ_ERR_HIP;
+  }
+  WQ_REQUIRE(dev >= 0 && dev < kMaxDevices, WQ_ERR_UNSUPPORTED, "device %d is beyond the %d this library tracks",
+             dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      return WQ_ERR_HIP;
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4_t*>(ptr),
+                       kNoAllocScratchBytes / 16);
+    if (int rc = check_launch("noalloc scratch clear")) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return WQ_OK;
+}
+
+}  // namespace
+}  // namespace wq
+
+extern "C" int wq_w4a16_linear_noalloc(const uint16_t* x, int64_t m, int64_t k, const void* tiles, const void* meta,
+                                       int64_t n, int64_t group_size, uint16_t* y, void* stream) {
+  if (int st = linear_shape_check(m, n, k)) return st;
+  if (m == 0) return wq_w4a16_linear(x, m, k, tiles, meta, n, group_size, y, nullptr, 0, stream);
+  const size_t need = gemv_workspace_bytes(true, m, n, k);
+  WQ_REQUIRE(need <= kNoAllocScratchBytes, WQ_ERR_WORKSPACE,
+             "wq_w4a16_linear_noalloc: m=%lld n=%lld k=%lld needs %zu scratch bytes, more than the %zu it holds",
+             (long long)m, (long long)n, (long long)k, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = noalloc_scratch(as_stream(stream), &ws)) return rc;
+  }
+  return wq_w4a16_linear(x, m, k, tiles, meta, n, group_size, y, ws, need, stream);
+}
