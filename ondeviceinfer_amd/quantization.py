@@ -1,8 +1,9 @@
 """Symmetric per-output-channel INT8 linear weights on MI355X.
 
-Mirrors ``ondeviceinfer/quantization.py``: the same format constants, the
-same validated ``QuantizedLinearWeight`` container and manifest, the same
-``FP16DequantScratch``, and the same functions.  The arithmetic runs in HIP:
+Keeps the callers' interface of ``ondeviceinfer/quantization.py``: the INT8
+v1 format constants and manifest entry, the validated
+``QuantizedLinearWeight`` container, ``FP16DequantScratch`` and the same
+functions and exceptions.  The arithmetic runs in HIP:
 
 * ``quantize_linear_weight`` -> ``wq_w8_quantize`` (bit-identical to the
   reference quantizer, ``quantization.py:226-285``);
@@ -33,89 +34,83 @@ QMIN = -127
 QMAX = 127
 
 
-def _state_key(prefix: str, suffix: str) -> str:
-    prefix = prefix.rstrip('.')
-    return f'{prefix}.{suffix}' if prefix else suffix
+def _join_key(prefix: str, leaf: str) -> str:
+    """``prefix.leaf`` (a trailing dot on the prefix is ignored; no prefix: ``leaf``)."""
+    return '.'.join(part for part in (prefix.rstrip('.'), leaf) if part)
 
 
-def _dtype_name(dtype: torch.dtype) -> str:
-    return str(dtype).removeprefix('torch.')
+def _check_all(rules) -> None:
+    """Raise the exception of the first rule ``(ok, exc_type, message)`` whose
+    condition is false; conditions may be callables, evaluated in order (the
+    value checks read device memory, so they run only after the cheap ones)."""
+    for ok, exc_type, message in rules:
+        if not (ok() if callable(ok) else ok):
+            raise exc_type(message)
 
 
 @dataclass(frozen=True)
 class QuantizedLinearWeight:
-    """``qweight`` int8 ``[out, in]`` and positive finite ``scale`` ``[out]``;
-    a row is ``qweight[row] * scale[row]`` (``quantization.py:37-158``)."""
+    """One linear weight in the INT8 v1 format: ``qweight`` int8 ``[out, in]``
+    and a strictly positive, finite floating-point ``scale [out]``; row ``r``
+    stands for ``qweight[r] * scale[r]`` (symmetric, zero point 0).  Same
+    fields, methods and errors as ``quantization.py:37-158``."""
 
     qweight: Tensor
     scale: Tensor
 
     def __post_init__(self) -> None:
-        if self.qweight.ndim != 2:
-            raise ValueError('qweight must have shape [out_features, in_features]')
-        if self.qweight.dtype != torch.int8:
-            raise TypeError('qweight must have dtype torch.int8')
-        if self.scale.ndim != 1 or self.scale.shape[0] != self.qweight.shape[0]:
-            raise ValueError('scale must have shape [out_features]')
-        if not self.scale.is_floating_point():
-            raise TypeError('scale must use a floating-point dtype')
-        if self.qweight.device != self.scale.device:
-            raise ValueError('qweight and scale must be on the same device')
-        if not bool(torch.isfinite(self.scale).all()):
-            raise ValueError('scale must contain only finite values')
-        if not bool((self.scale > 0).all()):
-            raise ValueError('scale values must be strictly positive')
+        q, s = self.qweight, self.scale
+        _check_all((
+            (q.dim() == 2, ValueError, 'qweight must have shape [out_features, in_features]'),
+            (q.dtype == torch.int8, TypeError, 'qweight must have dtype torch.int8'),
+            (s.dim() == 1 and s.shape[0] == q.shape[0], ValueError, 'scale must have shape [out_features]'),
+            (s.is_floating_point(), TypeError, 'scale must use a floating-point dtype'),
+            (q.device == s.device, ValueError, 'qweight and scale must be on the same device'),
+            (lambda: bool(torch.isfinite(s).all()), ValueError, 'scale must contain only finite values'),
+            (lambda: bool((s > 0).all()), ValueError, 'scale values must be strictly positive'),
+        ))
 
-    @property
-    def shape(self) -> torch.Size:
-        return self.qweight.shape
-
-    @property
-    def out_features(self) -> int:
-        return self.qweight.shape[0]
-
-    @property
-    def in_features(self) -> int:
-        return self.qweight.shape[1]
-
-    @property
-    def device(self) -> torch.device:
-        return self.qweight.device
+    shape = property(lambda self: self.qweight.shape)
+    out_features = property(lambda self: int(self.qweight.shape[0]))
+    in_features = property(lambda self: int(self.qweight.shape[1]))
+    device = property(lambda self: self.qweight.device)
 
     @property
     def storage_nbytes(self) -> int:
-        return self.qweight.nbytes + self.scale.nbytes
+        """Bytes of the INT8 codes plus the scales."""
+        return sum(t.numel() * t.element_size() for t in (self.qweight, self.scale))
+
+    def _map(self, fn) -> 'QuantizedLinearWeight':
+        return type(self)(qweight=fn(self.qweight), scale=fn(self.scale))
 
     def to(self, device, *, non_blocking: bool = False) -> 'QuantizedLinearWeight':
-        return type(self)(qweight=self.qweight.to(device=device, non_blocking=non_blocking),
-                          scale=self.scale.to(device=device, non_blocking=non_blocking))
+        """Both tensors on ``device``, dtypes unchanged."""
+        return self._map(lambda t: t.to(device=device, non_blocking=non_blocking))
 
     def pin_memory(self) -> 'QuantizedLinearWeight':
+        """Page-locked host copies (for asynchronous uploads); host weights only."""
         if self.device.type != 'cpu':
             raise ValueError('only CPU quantized weights can be pinned')
-        return type(self)(qweight=self.qweight.pin_memory(), scale=self.scale.pin_memory())
+        return self._map(Tensor.pin_memory)
 
     def tensor_dict(self, prefix: str = '') -> dict[str, Tensor]:
-        return {_state_key(prefix, 'qweight'): self.qweight, _state_key(prefix, 'scale'): self.scale}
+        """``{prefix.qweight, prefix.scale}``: the checkpoint keys."""
+        return {_join_key(prefix, leaf): getattr(self, leaf) for leaf in ('qweight', 'scale')}
 
     @classmethod
     def from_tensor_dict(cls, tensors: Mapping[str, Tensor], prefix: str = '') -> 'QuantizedLinearWeight':
-        return cls(qweight=tensors[_state_key(prefix, 'qweight')], scale=tensors[_state_key(prefix, 'scale')])
+        """Inverse of :meth:`tensor_dict`."""
+        return cls(**{leaf: tensors[_join_key(prefix, leaf)] for leaf in ('qweight', 'scale')})
 
     def manifest_entry(self, prefix: str = '') -> dict[str, Any]:
-        return {
-            'format': QUANTIZATION_FORMAT,
-            'version': QUANTIZATION_VERSION,
-            'axis': 0,
-            'zero_point': 0,
-            'quant_min': QMIN,
-            'quant_max': QMAX,
-            'shape': list(self.shape),
-            'qweight_key': _state_key(prefix, 'qweight'),
-            'scale_key': _state_key(prefix, 'scale'),
-            'qweight_dtype': _dtype_name(self.qweight.dtype),
-            'scale_dtype': _dtype_name(self.scale.dtype),
-        }
+        """The JSON record of this tensor in an INT8 v1 manifest."""
+        entry: dict[str, Any] = dict(_MANIFEST_CONSTANTS)
+        entry['shape'] = [int(d) for d in self.shape]
+        for leaf in ('qweight', 'scale'):
+            entry[f'{leaf}_key'] = _join_key(prefix, leaf)
+        for leaf in ('qweight', 'scale'):
+            entry[f'{leaf}_dtype'] = str(getattr(self, leaf).dtype).split('.')[-1]
+        return entry
 
     def dequantize(self, scratch: 'FP16DequantScratch | Tensor') -> Tensor:
         return dequantize_linear_weight(self, scratch)
@@ -124,49 +119,56 @@ class QuantizedLinearWeight:
         return quantized_linear(input, self, scratch, bias=bias)
 
 
+# Fields every INT8 v1 manifest entry carries, in the format's key order.
+_MANIFEST_CONSTANTS = (('format', QUANTIZATION_FORMAT), ('version', QUANTIZATION_VERSION), ('axis', 0),
+                       ('zero_point', 0), ('quant_min', QMIN), ('quant_max', QMAX))
+
+
 @dataclass
 class FP16DequantScratch:
-    """Reusable flat fp16 storage for one dequantized weight at a time
-    (``quantization.py:161-223``)."""
+    """A flat, contiguous fp16 buffer that holds one dequantized weight at a
+    time; any shape up to its capacity is a view of its head.  Same API as
+    ``quantization.py:161-223`` (reuse is ordered by the stream it is used on)."""
 
     buffer: Tensor
 
     def __post_init__(self) -> None:
-        if self.buffer.dtype != torch.float16:
-            raise TypeError('dequantization scratch must have dtype torch.float16')
-        if self.buffer.ndim != 1:
-            raise ValueError('dequantization scratch must be a flat tensor')
-        if not self.buffer.is_contiguous():
-            raise ValueError('dequantization scratch must be contiguous')
+        b = self.buffer
+        _check_all((
+            (b.dtype == torch.float16, TypeError, 'dequantization scratch must have dtype torch.float16'),
+            (b.dim() == 1, ValueError, 'dequantization scratch must be a flat tensor'),
+            (b.is_contiguous(), ValueError, 'dequantization scratch must be contiguous'),
+        ))
 
     @classmethod
     def allocate(cls, capacity: int, *, device) -> 'FP16DequantScratch':
         if capacity <= 0:
-            raise ValueError('scratch capacity must be positive')
+            raise ValueError(f'scratch capacity must be positive, got {capacity}')
         return cls(torch.empty(capacity, dtype=torch.float16, device=device))
 
     @classmethod
     def for_weights(cls, weights: Iterable[QuantizedLinearWeight], *, device=None) -> 'FP16DequantScratch':
-        weights = tuple(weights)
-        if not weights:
+        """Sized for the largest of ``weights``, on ``device`` (default: the first weight's)."""
+        sizes, first_device = [], None
+        for w in weights:
+            sizes.append(w.qweight.numel())
+            first_device = first_device or w.device
+        if not sizes:
             raise ValueError('at least one weight is required')
-        target = torch.device(device) if device is not None else weights[0].device
-        return cls.allocate(max(w.qweight.numel() for w in weights), device=target)
+        return cls.allocate(max(sizes), device=torch.device(device) if device is not None else first_device)
 
-    @property
-    def capacity(self) -> int:
-        return self.buffer.numel()
-
-    @property
-    def device(self) -> torch.device:
-        return self.buffer.device
+    capacity = property(lambda self: self.buffer.numel())
+    device = property(lambda self: self.buffer.device)
 
     def view_for(self, shape: Iterable[int]) -> Tensor:
-        shape = tuple(shape)
-        required = prod(shape)
-        if required > self.capacity:
-            raise ValueError(f'scratch capacity {self.capacity} is smaller than required {required}')
-        return self.buffer[:required].view(shape)
+        return _head_view(self.buffer, tuple(shape))
+
+
+def _head_view(flat: Tensor, shape: tuple) -> Tensor:
+    need = prod(shape)
+    if need > flat.numel():
+        raise ValueError(f'scratch capacity {flat.numel()} is smaller than required {need}')
+    return flat.narrow(0, 0, need).view(shape)
 
 
 @torch.no_grad()
@@ -202,16 +204,11 @@ def quantize_per_output_channel_int8(weight: Tensor, *, row_block_size: int = 25
 
 
 def _scratch_view(scratch: 'FP16DequantScratch | Tensor', shape: torch.Size) -> Tensor:
-    if isinstance(scratch, FP16DequantScratch):
-        return scratch.view_for(shape)
-    if scratch.dtype != torch.float16:
-        raise TypeError('dequantization scratch must have dtype torch.float16')
-    if not scratch.is_contiguous():
-        raise ValueError('dequantization scratch must be contiguous')
-    required = prod(shape)
-    if scratch.numel() < required:
-        raise ValueError(f'scratch capacity {scratch.numel()} is smaller than required {required}')
-    return scratch.view(-1)[:required].view(shape)
+    """``shape``-view of the head of a scratch object or of a raw fp16 tensor
+    (held to the same rules as ``FP16DequantScratch``)."""
+    if not isinstance(scratch, FP16DequantScratch):
+        scratch = FP16DequantScratch(scratch.view(-1) if scratch.is_contiguous() else scratch)
+    return scratch.view_for(shape)
 
 
 @torch.no_grad()

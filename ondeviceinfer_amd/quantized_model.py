@@ -92,7 +92,7 @@ import weakref  # noqa: E402
 import torch.nn.functional as F  # noqa: E402
 
 from .attention import cached_scaled_dot_product_attention, strided_prefill_attention  # noqa: E402
-from .cache import KVCache, ResidentKVCache  # noqa: E402
+from .cache import KVCache, ResidentKVCache, kv_block  # noqa: E402
 from .functional import add_rms_norm, rms_norm  # noqa: E402
 from .layers import RotaryEmbedding, apply_rotary_pos_emb  # noqa: E402
 
@@ -185,6 +185,30 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     return residual + mlp_output
 
 
+def _bind_int8_v1(layer: dict, ops) -> None:
+    """Give an INT8 v1 layer the prepared entries the decode graph runs:
+    per linear a ``PreparedW8`` over its ``qweight`` / fp16 ``scale``, then
+    q|k|v and gate|up concatenated (``fuse_projections``), after which the
+    parts' ``qweight`` / ``scale`` entries are rebound to views of the fused
+    copies so that no weight is held twice.  Values are unchanged, so the
+    eager ``int8_weight_only_linear`` path reads the same weights."""
+    from .weight_quantization.backend import PreparedW8
+    if not all(qweight_name(n) in layer for n in LINEAR_WEIGHT_NAMES) or QKV_FUSED.removesuffix('.weight') + \
+            '._prepared' in layer:
+        return
+    for name in LINEAR_WEIGHT_NAMES:
+        q = layer[qweight_name(name)]
+        s16 = layer[scale_name(name)].reshape(-1).half().contiguous()
+        layer[name.removesuffix('.weight') + '._prepared'] = PreparedW8(q.contiguous(), s16, int(q.shape[1]),
+                                                                       int(q.shape[0]))
+    ops.fuse_projections(layer)
+    for name in LINEAR_WEIGHT_NAMES:
+        p = layer[name.removesuffix('.weight') + '._prepared']
+        layer[qweight_name(name)] = p.qweight
+        if layer[scale_name(name)].dtype == torch.float16:
+            layer[scale_name(name)] = p.scale
+
+
 class DecodeStepGraph:
     """One batch-1 decode token of the whole model, captured once as a HIP
     graph over model-owned buffers: embedding row -> per layer [fused QKV
@@ -227,7 +251,8 @@ class DecodeStepGraph:
                                    dtype=torch.uint8, device=dev)
         self.scale = 1.0 / float(d) ** 0.5
         self.layers = [model.runtime.weights_for(i) for i in range(cfg.num_hidden_layers)]
-        calls = (model.linear_backend.calls, model.linear_backend.gemm_calls)
+        ops = model.graph_ops
+        calls = (ops.calls, ops.gemm_calls, model.compute_stats.linear_calls)
         for w in self.layers:
             for name in (QKV_FUSED, 'self_attn.o_proj.weight', GATE_UP_FUSED, 'mlp.down_proj.weight'):
                 if not _has_prepared(w, name):
@@ -248,11 +273,11 @@ class DecodeStepGraph:
         with torch.cuda.graph(self.graph):
             self._step()
         torch.cuda.synchronize(dev)
-        model.linear_backend.calls, model.linear_backend.gemm_calls = calls   # set-up launches are not calls
+        ops.calls, ops.gemm_calls, model.compute_stats.linear_calls = calls   # set-up launches are not calls
 
     def _linear(self, x: Tensor, weights: Mapping, name: str, out: Tensor) -> None:
         prepared = weights[name.removesuffix('.weight') + '._prepared']
-        self.model.linear_backend._fused(x, prepared, out)
+        self.model.graph_ops._fused(x, prepared, out)
 
     def _step(self) -> None:
         if self.fused:
@@ -331,8 +356,11 @@ class DecodeStepGraph:
         self.position.fill_(position)
         self.graph.replay()
         backend = self.model.linear_backend
-        backend.calls += 4 * len(self.layers)       # fused QKV, o, fused gate_up, down per layer
-        backend.gemm_calls += 4 * len(self.layers)
+        if backend is not None:
+            backend.calls += 4 * len(self.layers)       # fused QKV, o, fused gate_up, down per layer
+            backend.gemm_calls += 4 * len(self.layers)
+        else:   # INT8 v1: the reference counts its 7 linears per layer
+            self.model.compute_stats.linear_calls += 7 * len(self.layers)
         return self.logits
 
 
@@ -356,14 +384,27 @@ class QuantizedQwen3ForCausalLM:
         self.lm_head = store.lm_head.to(self.device)
         self.rotary_emb = RotaryEmbedding(self.config.head_dim, self.config.rope_theta).to(self.device)
         self.linear_backend = linear_backend
-        self.dequant_scratch = torch.empty(store.max_dequant_elements if linear_backend is None else 0,
-                                           device=self.device, dtype=self.dtype)
         self.compute_stats = QuantizedComputeStats(enabled=profile_compute)
-        self.decode_graph_enabled = decode_graph and linear_backend is not None and \
-            hasattr(linear_backend, 'fuse_projections')
-        if linear_backend is not None and hasattr(linear_backend, 'fuse_projections'):
+        if linear_backend is None:
+            # INT8 v1 weights (``prefix.qweight`` / ``prefix.scale``).  The
+            # reference dequantizes into an fp16 scratch of the largest
+            # matrix; the fused W8A16 kernel needs none, so the scratch is a
+            # zero-stride view with that element count (the capacity check of
+            # int8_weight_only_linear still applies).
+            self.dequant_scratch = torch.empty(1, device=self.device, dtype=self.dtype).expand(
+                store.max_dequant_elements)
+            from .weight_quantization.backend import CompressedLinearBackend
+            self.graph_ops = CompressedLinearBackend('w8a16')
             for idx in range(self.config.num_hidden_layers):
-                linear_backend.fuse_projections(runtime.weights_for(idx))
+                _bind_int8_v1(runtime.weights_for(idx), self.graph_ops)
+        else:
+            self.dequant_scratch = torch.empty(0, device=self.device, dtype=self.dtype)
+            self.graph_ops = linear_backend
+            if hasattr(linear_backend, 'fuse_projections'):
+                for idx in range(self.config.num_hidden_layers):
+                    linear_backend.fuse_projections(runtime.weights_for(idx))
+        self.decode_graph_enabled = decode_graph and hasattr(self.graph_ops, 'fuse_projections') and \
+            self.device.type == 'cuda'
         self._embed_device = None
         self._kv_pool: dict = {}
 
@@ -381,22 +422,19 @@ class QuantizedQwen3ForCausalLM:
         storage."""
         dev = torch.device(device or self.device)
         cfg = self.config
-        cache = ResidentKVCache(num_layers=0, batch_size=batch_size, num_key_value_heads=cfg.num_key_value_heads,
-                                max_seq_len=max_seq_len, head_dim=cfg.head_dim, device=dev, dtype=self.dtype)
         entries = self._kv_pool.setdefault((batch_size, max_seq_len, str(dev)), [])
         entry = next((e for e in entries if e['owner']() is None), None)
         if entry is None:
-            shape = (batch_size, cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
-            entry = {'k': [torch.zeros(shape, device=dev, dtype=self.dtype) for _ in range(cfg.num_hidden_layers)],
-                     'v': [torch.zeros(shape, device=dev, dtype=self.dtype) for _ in range(cfg.num_hidden_layers)],
-                     'graph': None}
+            block = kv_block(cfg.num_hidden_layers, batch_size, cfg.num_key_value_heads, max_seq_len, cfg.head_dim,
+                             device=dev, dtype=self.dtype, zero=True)
+            entry = {'block': block, 'graph': None}
             if self.decode_graph_enabled and batch_size == 1 and dev.type == 'cuda' and \
                     max_seq_len <= _native.DECODE_ATTENTION_MAX_SEQ:
-                entry['graph'] = DecodeStepGraph(self, entry['k'], entry['v'], max_seq_len)
+                view = ResidentKVCache.over(block)
+                entry['graph'] = DecodeStepGraph(self, view.key_cache, view.value_cache, max_seq_len)
             entries.append(entry)
+        cache = ResidentKVCache.over(entry['block'])
         entry['owner'] = weakref.ref(cache)
-        cache.key_cache, cache.value_cache = entry['k'], entry['v']
-        cache.lengths = [0] * cfg.num_hidden_layers
         cache._decode_graph = entry['graph']
         return cache
 

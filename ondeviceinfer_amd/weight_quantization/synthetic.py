@@ -117,6 +117,40 @@ def random_compressed_store(cfg: Qwen3Config, *, seed: int = 0, device: str | to
     return CompressedStore(cfg, layers, embed, final_norm, lm_head, manifest)
 
 
+def random_int8_store(cfg: Qwen3Config, *, seed: int = 0, device: str | torch.device = 'cuda:0',
+                      std: float = 0.02):
+    """A random INT8 v1 Qwen3 model (``QuantizedCpuWeightStore``): every
+    decoder linear drawn as ``fp16(N(0, std))`` and quantized per output
+    channel by the GPU quantizer (``wq_w8_quantize``, the reference's
+    ``quantize_linear_weight`` bit for bit); ``prefix.qweight`` /
+    ``prefix.scale`` and the norms stay on ``device``, the embedding / final
+    norm / LM head on the host."""
+    from .. import _native
+    from ..runtime.quantized import QuantizedCpuWeightStore, qweight_name, scale_name
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cpu_gen = torch.Generator().manual_seed(seed + 1)
+    layers = []
+    for _ in range(cfg.num_hidden_layers):
+        layer = {}
+        for name, (n, k) in linear_shapes(cfg).items():
+            w = (torch.randn((n, k), device=device, generator=gen) * std).half()
+            layer[qweight_name(name)], layer[scale_name(name)] = _native.w8_quantize(w)
+            del w
+        for name in NORM_WEIGHT_NAMES:
+            size = cfg.head_dim if 'q_norm' in name or 'k_norm' in name else cfg.hidden_size
+            layer[name] = (1.0 + 0.1 * torch.randn(size, device=device, generator=gen)).half()
+        layers.append(layer)
+    embed = (torch.randn(cfg.vocab_size, cfg.hidden_size, device=device, generator=gen) * 0.02).half().cpu()
+    lm_head = embed if cfg.tie_word_embeddings else \
+        (torch.randn(cfg.vocab_size, cfg.hidden_size, device=device, generator=gen) * 0.02).half().cpu()
+    final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden_size, generator=cpu_gen)).half()
+    return QuantizedCpuWeightStore(config=cfg, layers=layers, embed_tokens=embed, final_norm=final_norm,
+                                   lm_head=lm_head, compute_dtype=torch.float16,
+                                   manifest={'format': 'qwen3-int8-weight-only-v1', 'source': 'synthetic',
+                                             'seed': seed, 'weight_std': std})
+
+
 def quantization_config(group_size: int, symmetric: bool) -> dict:
     """compressed-tensors ``quantization_config`` for W4A16 pack-quantized."""
     return {
@@ -171,5 +205,5 @@ def write_compressed_checkpoint(path: str | Path, store: CompressedStore, *, lay
     return path
 
 
-__all__ = ['awq_quantize', 'linear_shapes', 'pack_nibbles', 'random_compressed_store', 'quantization_config', 'write_compressed_checkpoint',
+__all__ = ['awq_quantize', 'linear_shapes', 'pack_nibbles', 'random_compressed_store', 'random_int8_store', 'quantization_config', 'write_compressed_checkpoint',
            'LINEAR_WEIGHT_NAMES']

@@ -192,6 +192,32 @@ def test_w4a16_config4_batch_sweep(gpu, name, n, ncols):
         check_parity(y[:, cols], qdq.linear_fp32(x[:m], w_cols), f'w4 {name} {k}->{n} m={m}')
 
 
+def test_bitwise_repeatability_of_the_decoder_linears(gpu):
+    """The reference harness's determinism check (``validate_weight_quant_kernels.py:49-70``):
+    each of the 7 Qwen3-14B decoder linears at M in {1, 4, 32, 256}, 20 repeated calls
+    on the same input compared bit for bit with the first (decode GEMV with its
+    k-split reduction, skinny kernels, GEMM)."""
+    from ondeviceinfer_amd.weight_quantization.synthetic import awq_quantize
+    shapes = {'self_attn.q_proj.weight': (5120, 5120), 'self_attn.k_proj.weight': (1024, 5120),
+              'self_attn.v_proj.weight': (1024, 5120), 'self_attn.o_proj.weight': (5120, 5120),
+              'mlp.gate_proj.weight': (17408, 5120), 'mlp.up_proj.weight': (17408, 5120),
+              'mlp.down_proj.weight': (5120, 17408)}
+    gen = torch.Generator(device=gpu).manual_seed(0)
+    backend = wq.CompressedLinearBackend('marlin')
+    changes = {}
+    for name, (n, k) in shapes.items():
+        w = (torch.randn(n, k, generator=gen, device=gpu) * 0.02).half()
+        layer = {f"{name.removesuffix('.weight')}.{key}": v.to(gpu) for key, v in awq_quantize(w).items()}
+        backend.prepare(layer, name)
+        for m in (1, 4, 32, 256):
+            x = torch.randn(m, k, generator=gen, device=gpu).half()
+            first = backend.linear(x, layer, name).clone()
+            changes[(name, m)] = sum(int(not torch.equal(backend.linear(x, layer, name), first)) for _ in range(20))
+            assert torch.isfinite(first).all()
+    print('bitwise changes over 20 repeats:', changes, flush=True)
+    assert not any(changes.values()), changes
+
+
 def test_w4a16_repeat_calls_are_bitwise_identical(gpu):
     name = 'mlp.down_proj.weight'
     weights, x = synth.w4_case(5120, 17408, 4, seed=3, name=name)
