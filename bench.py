@@ -5,7 +5,8 @@ Headline (the workload the metric's published number is
 quoted on): batch 1, a 4096-token random prompt, greedy decode with the fp16
 KV cache resident, random-init weights of the Qwen3-14B architecture (40
 layers, hidden 5120, 40/8 heads of 128, SwiGLU 17408, vocab 151936), the
-decoder linears uint4 with fp16 group-128 scales and zero points.  One *step*
+decoder linears drawn as fp16 N(0, 0.02) and quantized to uint4 with fp16
+group-128 scales and zero points (asymmetric min-max RTN).  One *step*
 is one decode token: a replay of the captured decode-step graph (40 x [QKV
 GEMV with the input RMSNorm in its prologue, attention (q/k norm, RoPE, cache
 append, GQA) + chunk merge, o GEMV + residual, gate_up GEMV with the
@@ -27,11 +28,19 @@ Also in the same JSON line:
 * ``prefill``: the M=4096 W4A16 GEMM (configs[2]) per shape, TFLOP/s;
 * ``batch_sweep``: fused QKV, fused gate_up and a W4 lm_head at
   M in {1, 8, 32, 128, 512}, GB/s and TFLOP/s per launch;
-* ``int8``: configs[0]'s INT8 weight on the GPU: weight-only W8A16 decode GB/s,
-  and W8A8 (``int8_gemm``) decode GB/s and M=4096 TOPS vs the int8 MFMA peak;
+* ``int8``: configs[0]'s INT8 weight shape on the GPU over a pool of 40
+  distinct weights (1.05 GB, past the 256 MB Infinity Cache): weight-only
+  W8A16 and W8A8 (``int8_gemm``) decode GB/s, M=4096 W8A16 TFLOP/s and W8A8
+  TOPS against the fp16 / int8 MFMA peaks;
+* ``int8_e2e``: the INT8 weight-only model (INT8 v1 tensors, the reference's
+  first published row) on the same workload, tok/s;
+* ``setup_seconds``: weight generation, the whole-model repack and the
+  startup repack of each of layer 0's linears;
 * ``copy_ceiling``: a device-to-device copy's GB/s on the same box;
-* ``cpu_baseline``: the numpy QDQ oracle on one decoder layer's decode work,
-  scaled to tok/s for the 40-layer model.
+* ``cpu_baseline``: the explicit QDQ path in torch on the host CPU, all
+  available threads (oracle/qdq_torch.py), per call on configs[0] and each
+  configs[1] shape at M=1 (ms, GB/s), and the tok/s those calls give for the
+  40 layers' linears.
 """
 from __future__ import annotations
 
@@ -53,6 +62,8 @@ INT8_MFMA_PEAK_TOPS = 5000.0      # dense int8 MFMA, MI355X
 GROUP = 128
 PROMPT = 4096
 HIDDEN, INTER, KV, QKV, GATE_UP = 5120, 17408, 1024, 7168, 34816
+LINEAR_NAMES = ('self_attn.q_proj.weight', 'self_attn.k_proj.weight', 'self_attn.v_proj.weight',
+                'self_attn.o_proj.weight', 'mlp.gate_proj.weight', 'mlp.up_proj.weight', 'mlp.down_proj.weight')
 LAYER_SHAPES = [  # (name, K, N) in decoder order
     ('self_attn.q_proj', HIDDEN, HIDDEN), ('self_attn.k_proj', HIDDEN, KV), ('self_attn.v_proj', HIDDEN, KV),
     ('self_attn.o_proj', HIDDEN, HIDDEN), ('mlp.gate_proj', HIDDEN, INTER), ('mlp.up_proj', HIDDEN, INTER),
@@ -120,39 +131,118 @@ def profiled_traffic(kernel: str, shape: str):
     return None if rec is None else int(rec['hbm_bytes_per_launch'])
 
 
-def cpu_baseline(budget_s: float, layers: int) -> dict:
-    """The numpy QDQ oracle (decode_weight + fp32 GEMV, one BLAS thread) on one
-    decoder layer's decode-token work, scaled to tok/s for `layers` layers."""
+def host_threads() -> int:
+    """CPU threads this process may use: its affinity set, capped by
+    OMP_NUM_THREADS when the launcher sets it (the GPU boxes give each job a
+    16-CPU share and say so there)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, 'sched_getaffinity') else (os.cpu_count() or 1)
+    omp = os.environ.get('OMP_NUM_THREADS', '')
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path('/proc/cpuinfo').read_text().splitlines():
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def cpu_baseline(torch, native, device, layers: int) -> dict:
+    """The reference's explicit QDQ path on the host CPU with torch
+    (oracle/qdq_torch.py: decode_weight + fp32-accumulated F.linear), all
+    available threads: configs[0] (INT8 5120x5120 per-channel, M = 1) and each
+    configs[1] W4A16 G=128 shape at M = 1; 3 warm-up calls, then the median
+    of 10 timed calls per shape.  ``value`` is the tok/s those per-call
+    times give for the 7 decoder linears of `layers` layers (the linears
+    only: no attention, norms or LM head)."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
-    from oracle import qdq, qwen3, synth
-    cases = []
-    for name, k, n in LAYER_SHAPES:
-        w, x = synth.w4_case(n, k, 1, seed=0, name=f'{name}.weight')
-        cases.append((name, w, x))
-    rng = np.random.default_rng(0)
-    q = rng.standard_normal((40, 1, 128)).astype(np.float16)
-    kc = rng.standard_normal((8, PROMPT, 128)).astype(np.float16)
-    vc = rng.standard_normal((8, PROMPT, 128)).astype(np.float16)
-    times = []
-    with threadpool_limits(limits=1):
-        t_begin = time.perf_counter()
-        while True:
+    from oracle import qdq_torch
+    from ondeviceinfer_amd.weight_quantization.synthetic import awq_quantize
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    gen = torch.Generator(device=device).manual_seed(0)
+    cpu_gen = torch.Generator().manual_seed(0)
+
+    def timed(fn) -> tuple[float, int]:
+        for _ in range(3):
+            fn()
+        runs = []
+        for _ in range(10):
             t0 = time.perf_counter()
-            for name, w, x in cases:
-                qdq.qdq_linear(x, w, f'{name}.weight')
-            qwen3.attention(q, kc, vc, None)
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - t_begin > budget_s or len(times) >= 10:
-                break
-    sec = float(np.median(times))
-    per_token = sec * layers
-    return {'value': round(1.0 / per_token, 6), 'unit': 'tok/s', 'cores': 1, 'kind': 'port',
-            'sample': f'one decoder layer of the decode token on the host: oracle.qdq.qdq_linear (numpy '
-                      f'decode_weight + fp32 GEMV) over the 7 W4A16 projections at M=1 plus oracle.qwen3.attention '
-                      f'over a {PROMPT}-row KV cache, 1 BLAS thread, median of {len(times)} passes = {sec:.3f} s; '
-                      f'x {layers} layers (LM head, norms and RoPE not included)',
-            'seconds_per_layer': round(sec, 3), 'host_cpu_count': os.cpu_count()}
+            fn()
+            runs.append(time.perf_counter() - t0)
+        return float(np.median(runs)), len(runs)
+
+    shapes = []
+    w = (torch.randn(HIDDEN, HIDDEN, device=device, generator=gen) * 0.02).half()
+    q8, s8 = (t.cpu() for t in native.w8_quantize(w))
+    x = torch.randn(1, HIDDEN, generator=cpu_gen).half()
+    sec, runs = timed(lambda: qdq_torch.int8_qdq_linear(x, q8, s8))
+    b = HIDDEN * HIDDEN + 2 * HIDDEN + 2 * HIDDEN + 2 * HIDDEN
+    shapes.append({'config': 'configs[0]', 'op': 'INT8 per-channel QDQ linear', 'shape': f'{HIDDEN}->{HIDDEN}', 'M': 1,
+                   'ms_per_call': round(sec * 1e3, 3), 'gbs': round(b / sec / 1e9, 2), 'algorithmic_bytes': b,
+                   'runs': runs})
+    per_shape = {}
+    for name, k, n in LAYER_SHAPES:
+        if (k, n) in per_shape:
+            continue
+        w = (torch.randn(n, k, device=device, generator=gen) * 0.02).half()
+        weights = {f'p.{key}': v.cpu() for key, v in awq_quantize(w).items()}
+        del w
+        x = torch.randn(1, k, generator=cpu_gen).half()
+        sec, runs = timed(lambda: qdq_torch.qdq_linear(x, weights, 'p.weight'))
+        per_shape[(k, n)] = sec
+        b = w4_bytes(1, n, k)
+        shapes.append({'config': 'configs[1]', 'op': 'W4A16 G=128 QDQ linear', 'shape': f'{k}->{n}', 'M': 1,
+                       'ms_per_call': round(sec * 1e3, 3), 'gbs': round(b / sec / 1e9, 2), 'algorithmic_bytes': b,
+                       'runs': runs})
+    per_token = layers * sum(per_shape[(k, n)] for _, k, n in LAYER_SHAPES)
+    return {'value': round(1.0 / per_token, 4), 'unit': 'tok/s', 'cores': threads, 'kind': 'port',
+            'sample': f'torch {torch.__version__} on the host CPU ({threads} threads): the explicit QDQ path '
+                      '(oracle/qdq_torch.py) at M=1 on configs[0] and each configs[1] shape, median of 10 calls '
+                      f'after 3 warm-ups; value = 1 / ({layers} layers x the 7 decoder linears), linears only',
+            'shapes': shapes, 'cpu_model': cpu_model(), 'os_cpu_count': os.cpu_count(),
+            'omp_num_threads': os.environ.get('OMP_NUM_THREADS')}
+
+
+def int8_e2e(torch, layers: int, device, steps: int, warmup: int) -> dict:
+    """The reference's first published row on this build: the INT8 weight-only
+    model (INT8 v1 tensors, linear_backend=None) decoding after a 4096-token
+    prompt, B=1, each token one replay of its captured decode graph
+    (fused W8A16 GEMVs that read the INT8 weights once)."""
+    from ondeviceinfer_amd.config import QWEN3_14B, Qwen3Config
+    from ondeviceinfer_amd.quantized_model import QuantizedQwen3ForCausalLM
+    from ondeviceinfer_amd.runtime.quantized import QuantizedResidentRuntime
+    from ondeviceinfer_amd.weight_quantization.synthetic import random_int8_store
+    from ondeviceinfer_amd.generation import greedy_token
+    cfg = Qwen3Config.from_dict(dict(QWEN3_14B, num_hidden_layers=layers))
+    store = random_int8_store(cfg, seed=0, device=device)
+    model = QuantizedQwen3ForCausalLM(store, QuantizedResidentRuntime(store, device=device), device=device)
+    prompt = torch.randint(0, cfg.vocab_size, (1, PROMPT), generator=torch.Generator().manual_seed(0)).to(device)
+    cache = model.make_resident_cache(batch_size=1, max_seq_len=PROMPT + 1 + warmup + steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    token = greedy_token(model(prompt, cache=cache, logits_to_keep=1))
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for _ in range(warmup):
+        token = greedy_token(model(token, cache=cache, logits_to_keep=1))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        token = greedy_token(model(token, cache=cache, logits_to_keep=1))
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    return {'workload': f'INT8 per-channel weight-only Qwen3-14B-shaped decoder ({layers} layers, INT8 v1 tensors), '
+                        f'B=1, {PROMPT}-token prompt, greedy decode, fp16 KV resident; decode graph of W8A16 GEMVs',
+            'tok_s': round(steps / sec, 2), 'ms_per_token': round(sec * 1e3 / steps, 4), 'steps': steps,
+            'prefill_seconds': round(prefill_s, 4), 'decoder_int8_bytes': store.decoder_bytes,
+            'vs_reference_int8_explicit_path': round(steps / sec / 5.326, 2)}
 
 
 def build_model(torch, layers: int, device):
@@ -161,12 +251,35 @@ def build_model(torch, layers: int, device):
     from ondeviceinfer_amd.weight_quantization.backend import CompressedLinearBackend, CompressedResidentRuntime
     from ondeviceinfer_amd.weight_quantization.synthetic import random_compressed_store
     cfg = Qwen3Config.from_dict(dict(QWEN3_14B, num_hidden_layers=layers))
+    t0 = time.perf_counter()
     store = random_compressed_store(cfg, seed=0, device=device)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    # The startup repack per linear (the reference records repack_seconds,
+    # validate_weight_quant_kernels.py:46-48): layer 0's seven linears.
+    probe = CompressedLinearBackend('marlin')
+    repack_ms = {}
+    for name in LINEAR_NAMES:
+        prefix = name.removesuffix('.weight')
+        layer = {k: v for k, v in store.layers[0].items() if k.startswith(prefix + '.')}
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        probe.prepare(layer, name)
+        torch.cuda.synchronize()
+        repack_ms[prefix] = round((time.perf_counter() - t) * 1e3, 3)
+        del layer
     backend = CompressedLinearBackend('marlin')
+    t2 = time.perf_counter()
     runtime = CompressedResidentRuntime(store, backend, device=device, verbose=False)
     model = QuantizedQwen3ForCausalLM(store, runtime, device=device, linear_backend=backend)
     torch.cuda.synchronize()
-    return cfg, model, runtime
+    t3 = time.perf_counter()
+    # prepare() keeps only the repacked tiles (backend.py:224-226); drop the
+    # store's raw copies as well.
+    store.layers = [{} for _ in store.layers]
+    setup = {'random_weights_and_awq_quantize': round(t1 - t0, 2), 'repack_all_layers_and_fuse': round(t3 - t2, 3),
+             'repack_ms_per_linear_layer0': repack_ms}
+    return cfg, model, runtime, setup
 
 
 def main() -> int:
@@ -175,7 +288,6 @@ def main() -> int:
     ap.add_argument('--steps', type=int, default=127, help='timed decode tokens')
     ap.add_argument('--warmup', type=int, default=5, help='untimed decode tokens before the timed ones')
     ap.add_argument('--layers', type=int, default=40)
-    ap.add_argument('--cpu-budget', type=float, default=15.0, help='seconds for the CPU baseline sample')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-extras', action='store_true', help='skip the GEMV pass, kernel and prefill sections')
     args = ap.parse_args()
@@ -199,7 +311,7 @@ def main() -> int:
 
     log(f'building a random {args.layers}-layer Qwen3-14B-shaped W4A16 model and repacking it')
     t0 = time.perf_counter()
-    cfg, model, runtime = build_model(torch, args.layers, device)
+    cfg, model, runtime, setup = build_model(torch, args.layers, device)
     build_s = time.perf_counter() - t0
     capacity = PROMPT + 1 + args.warmup + args.steps
     prompt = torch.randint(0, cfg.vocab_size, (1, PROMPT), generator=torch.Generator().manual_seed(0)).to(device)
@@ -249,7 +361,7 @@ def main() -> int:
         'bytes_per_token': {'decoder_weights': int(weight_bytes), 'lm_head_fp16': lm_bytes,
                             'kv_cache_read_at_start': kv_bytes_per_token},
         'effective_gbs': round((weight_bytes + lm_bytes + kv_bytes_per_token) * toks / 1e9, 1),
-        'setup_seconds': {'build_and_repack': round(build_s, 2), 'graph_capture': round(capture_s, 3)},
+        'setup_seconds': {'build_and_repack': round(build_s, 2), 'graph_capture': round(capture_s, 3), **setup},
     }
     result['pct_hbm_peak_effective'] = round(100.0 * result['effective_gbs'] / HBM_PEAK_GBS, 2)
     del cache
@@ -451,13 +563,17 @@ def main() -> int:
         result['batch_sweep'] = sweep
         del lm_tiles, lm_meta
 
-        # INT8 variants on configs[0]'s weight (5120 x 5120, N(0, 0.02), per-channel
-        # symmetric INT8): weight-only W8A16 decode, and W8A8 (int8_gemm) decode
-        # and M=4096 prefill on the int8 matrix cores.
+        # INT8 variants of configs[0] on the GPU over a pool of 40 distinct
+        # 5120x5120 weights (N(0, 0.02), per-channel symmetric INT8; 1.05 GB,
+        # above the 256 MB Infinity Cache), each case a graph of one launch
+        # per weight: weight-only W8A16 decode, W8A8 (int8_gemm) decode and
+        # the M=4096 W8A16 / W8A8 prefill GEMMs on the matrix cores.
         g0 = torch.Generator(device=device).manual_seed(0)
-        w8 = (torch.randn(HIDDEN, HIDDEN, device=device, generator=g0) * 0.02).float()
-        q8w, s8w = native.w8_quantize(w8)
-        s8w32 = s8w.float()
+        pool = []
+        for _ in range(40):
+            w8 = (torch.randn(HIDDEN, HIDDEN, device=device, generator=g0) * 0.02).half()
+            q8w, s8w = native.w8_quantize(w8)
+            pool.append((q8w, s8w, s8w.float()))
         del w8
         int8 = []
         x1 = torch.randn(1, HIDDEN, device=device).half()
@@ -467,32 +583,38 @@ def main() -> int:
         y1 = torch.empty(1, HIDDEN, device=device, dtype=torch.float16)
         y4k = torch.empty(4096, HIDDEN, device=device, dtype=torch.float16)
         cases = [
-            ('w8a16 decode (configs[0] on the GPU)', 1, lambda: native.w8a16_linear(x1, q8w, s8w, out=y1)),
-            ('w8a8 int8_gemm decode (quantize + linear)', 1,
-             lambda: native.w8a8_linear(*native.w8a8_quantize(x1), q8w, s8w32, out=y1)),
-            ('w8a8 linear only, decode', 1, lambda: native.w8a8_linear(qx1, sx1, q8w, s8w32, out=y1)),
-            ('w8a8 linear only, prefill M=4096', 4096, lambda: native.w8a8_linear(qx4k, sx4k, q8w, s8w32, out=y4k)),
+            ('w8a16 decode (configs[0] on the GPU)', 1, 'w8a16',
+             lambda q, s, s32: native.w8a16_linear(x1, q, s, out=y1)),
+            ('w8a8 int8_gemm decode (quantize + linear)', 1, 'w8a8',
+             lambda q, s, s32: native.w8a8_linear(*native.w8a8_quantize(x1), q, s32, out=y1)),
+            ('w8a8 linear only, decode', 1, 'w8a8', lambda q, s, s32: native.w8a8_linear(qx1, sx1, q, s32, out=y1)),
+            ('w8a16 prefill M=4096', 4096, 'w8a16', lambda q, s, s32: native.w8a16_linear(x4k, q, s, out=y4k)),
+            ('w8a8 linear only, prefill M=4096', 4096, 'w8a8',
+             lambda q, s, s32: native.w8a8_linear(qx4k, sx4k, q, s32, out=y4k)),
         ]
-        for label, mm, fn in cases:
-            fn()
+        for label, mm, kind, fn in cases:
+            fn(*pool[0])
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                for _ in range(10):
-                    fn()
-            sec = time_graph(torch, g, 10) / 10
-            w8a8 = 'w8a8' in label   # int8 x and fp32 scales vs fp16 x and fp16 scales
+                for q8w, s8w, s32 in pool:
+                    fn(q8w, s8w, s32)
+            sec = time_graph(torch, g, 5) / len(pool)
+            w8a8 = kind == 'w8a8'   # int8 x and fp32 scales vs fp16 x and fp16 scales
             b = HIDDEN * HIDDEN + (4 if w8a8 else 2) * HIDDEN + (1 if w8a8 else 2) * mm * HIDDEN + 2 * mm * HIDDEN
-            entry = {'op': label, 'shape': f'{HIDDEN}->{HIDDEN}', 'M': mm, 'us': round(sec * 1e6, 2)}
+            entry = {'op': label, 'shape': f'{HIDDEN}->{HIDDEN}', 'M': mm, 'us': round(sec * 1e6, 2),
+                     'weights_rotated': len(pool), 'pool_bytes': len(pool) * HIDDEN * HIDDEN}
             if mm == 1:
                 entry.update(gbs=round(b / sec / 1e9, 1), frac_hbm=round(b / sec / 1e9 / HBM_PEAK_GBS, 4),
                              algorithmic_bytes=b)
             else:
                 tops = 2 * mm * HIDDEN * HIDDEN / sec / 1e12
-                entry.update(tops=round(tops, 1), frac_int8_mfma=round(tops / INT8_MFMA_PEAK_TOPS, 4))
+                peak = INT8_MFMA_PEAK_TOPS if w8a8 else FP16_MFMA_PEAK_TFLOPS
+                entry.update(tops=round(tops, 1), frac_mfma_peak=round(tops / peak, 4),
+                             mfma_peak='int8 5.0 POP/s' if w8a8 else 'fp16 2.5 PFLOP/s')
             int8.append(entry)
             del g
         result['int8'] = int8
-        del q8w, s8w, s8w32, x4k, qx4k, y4k
+        del pool, x4k, qx4k, y4k
 
         # Copy ceiling: 2 GiB device-to-device copy (read + write bytes).
         src = torch.empty(2**30, dtype=torch.uint16, device=device)
@@ -510,9 +632,14 @@ def main() -> int:
                                   'how': 'torch copy_ of 2 GiB, read+write bytes / time'}
         del src, dst
 
+    if not args.no_extras:
+        log('INT8 weight-only model: build, prefill and decode')
+        result['int8_e2e'] = int8_e2e(torch, args.layers, device, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+
     if not args.no_cpu_baseline:
         log('cpu baseline')
-        result['cpu_baseline'] = cpu_baseline(args.cpu_budget, args.layers)
+        result['cpu_baseline'] = cpu_baseline(torch, native, device, args.layers)
 
     print(json.dumps(result), flush=True)
     return 0

@@ -301,3 +301,46 @@ def test_w8a8_scaled_int_gemm_brute_force():
             assert got[m, n] == np.float16(np.float32(r))
     # the largest magnitude a Qwen3 shape produces still fits int32
     assert 127 * 127 * 17408 < 2 ** 31
+
+
+# ------------------------------------------------------------------- torch-CPU restatement (bench baseline)
+
+def _torch_weights(weights):
+    import torch
+    return {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in weights.items()}
+
+
+@pytest.mark.parametrize('sym', [False, True])
+def test_torch_qdq_decode_is_bit_identical_to_the_numpy_oracle(sym):
+    from oracle import qdq_torch
+    weights, x = synth.w4_case(48, 512, 3, seed=11, symmetric=sym, name='p.weight')
+    got = qdq_torch.decode_weight(_torch_weights(weights), 'p.weight').numpy()
+    assert np.array_equal(got.view(np.uint16), qdq.decode_weight(weights, 'p.weight').view(np.uint16))
+    y = qdq_torch.qdq_linear(_torch_weights({'x': x})['x'], _torch_weights(weights), 'p.weight').numpy()
+    assert qdq.parity_ok(qdq.parity_metrics(y, qdq.qdq_linear(x, weights, 'p.weight')))
+    assert np.abs(y.astype(np.float32) - qdq.qdq_linear(x, weights, 'p.weight').astype(np.float32)).max() <= \
+        2 ** -10 * np.abs(y).max()
+
+
+def test_torch_qdq_int8_matches_the_numpy_oracle():
+    import torch
+    from oracle import qdq_torch
+    _, q, s, x = synth.int8_case(40, 256, 2, seed=12)
+    ct = {'p.weight': torch.from_numpy(q), 'p.weight_scale': torch.from_numpy(s).reshape(-1, 1)}
+    assert np.array_equal(qdq_torch.decode_weight(ct, 'p.weight').numpy().view(np.uint16),
+                          qdq.dequantize_linear_weight(q, s).view(np.uint16))
+    y = qdq_torch.int8_qdq_linear(torch.from_numpy(x), torch.from_numpy(q), torch.from_numpy(s)).numpy()
+    assert qdq.parity_ok(qdq.parity_metrics(y, qdq.int8_weight_only_linear(x, q, s)))
+    # the KAT of test_weight_quant_backend.py:33-35 through the torch decode
+    kat = {'p.weight': torch.tensor([[2, -3]], dtype=torch.int8), 'p.weight_scale': torch.tensor([[0.5]]).half()}
+    assert qdq_torch.decode_weight(kat, 'p.weight').tolist() == [[1.0, -1.5]]
+
+
+def test_torch_unpack_matches_kat_words():
+    import torch
+    from oracle import qdq_torch
+    word = torch.tensor([[0x76543210]], dtype=torch.int32)
+    assert qdq_torch.unpack_unsigned(word, 4, 1, 8).tolist() == [[0, 1, 2, 3, 4, 5, 6, 7]]
+    assert qdq_torch.unpack_unsigned(word, 4, 0, 8).t().tolist() == [[0, 1, 2, 3, 4, 5, 6, 7]]
+    neg = torch.tensor([[-1]], dtype=torch.int32)     # sign bits must not leak into the top field
+    assert qdq_torch.unpack_unsigned(neg, 4, 1, 8).tolist() == [[15] * 8]
