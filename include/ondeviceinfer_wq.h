@@ -85,6 +85,16 @@ int wq_w4_decode(const int32_t* weight_packed, const float* weight_scale,
                  int64_t n, int64_t k, int64_t num_groups, int64_t group_size,
                  uint16_t* weight, void* stream);
 
+/* Row-sampled form of wq_w4_decode: weight [num_rows, k] row r =
+ * fp16((q - z) * s) of source row rows[r] (int64, each in [0, n): the host
+ * checks), groups of group_size along k (no g_idx).  Replaces decode_rows
+ * (benchmarks/validate_weight_reconstruction.py:20-31), which samples the
+ * rows of a large matrix such as the LM head instead of decoding it whole. */
+int wq_w4_decode_rows(const int32_t* weight_packed, const float* weight_scale,
+                      const int32_t* weight_zero_point, const int64_t* rows, int64_t num_rows,
+                      int64_t n, int64_t k, int64_t num_groups, int64_t group_size,
+                      uint16_t* weight, void* stream);
+
 /* Workspace bytes wq_w4a16_linear can use for this shape (0 when it needs
  * none).  The workspace holds the per-tile counters and fp32 partials of the
  * decode GEMV when a tile's k range is split over several workgroups.  It must

@@ -46,6 +46,7 @@ _SIGNATURES = {
     'wq_w4_unpack': [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P],
     'wq_w4_dequant': [_P, _P, _I64, _I64, _I64, _P, _P],
     'wq_w4_decode': [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P],
+    'wq_w4_decode_rows': [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     'wq_w4a16_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
     'wq_w4a16_linear': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, ctypes.c_size_t, _P],
     'wq_w4a16_linear_noalloc': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P],
@@ -227,6 +228,28 @@ def w4_decode(packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor | No
     out = torch.empty((n, k), dtype=torch.float16, device=device)
     _call('wq_w4_decode', _ptr(packed), _ptr(scale32), _ptr(zero), _ptr(gi), n, k, scale32.shape[1], group_size,
           _ptr(out), _stream(device))
+    return out
+
+
+def w4_decode_rows(packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor | None, rows: torch.Tensor,
+                   n: int, k: int, group_size: int = 128) -> torch.Tensor:
+    """fp16 ``[len(rows), k]``: the explicit decode of the given rows only."""
+    device = _require_gpu(packed, scale, zero, rows)
+    if packed.dtype != torch.int32 or tuple(packed.shape) != (n, k // 8) or k % 8:
+        raise ValueError(f'weight_packed must be int32 [{n}, {k // 8}], got {packed.dtype} {tuple(packed.shape)}')
+    scale32 = scale.float().contiguous()
+    if scale32.dim() != 2 or scale32.shape[0] != n:
+        raise ValueError(f'weight_scale must be [{n}, groups], got {tuple(scale.shape)}')
+    if zero is not None:
+        if zero.dtype != torch.int32 or tuple(zero.shape) != ((n + 7) // 8, scale32.shape[1]):
+            raise ValueError(f'weight_zero_point must be int32 [{(n + 7) // 8}, {scale32.shape[1]}]')
+        zero = zero.contiguous()
+    idx = rows.reshape(-1).to(device=device, dtype=torch.int64).contiguous()
+    if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= n):
+        raise IndexError(f'row indices must lie in [0, {n})')
+    out = torch.empty((idx.numel(), k), dtype=torch.float16, device=device)
+    _call('wq_w4_decode_rows', _ptr(packed.contiguous()), _ptr(scale32), _ptr(zero), _ptr(idx), idx.numel(), n, k,
+          scale32.shape[1], group_size, _ptr(out), _stream(device))
     return out
 
 

@@ -172,6 +172,34 @@ __global__ void w4_decode_kernel(const uint32_t* __restrict__ packed, const floa
   *reinterpret_cast<uint4_t*>(out + idx * 8) = o;
 }
 
+// Row-sampled explicit decode: output row r is weight row rows[r] (one thread
+// per source word of a sampled row), groups of `group_size` along k.
+__global__ void w4_decode_rows_kernel(const uint32_t* __restrict__ packed, const float* __restrict__ scale,
+                                      const uint32_t* __restrict__ zero, const int64_t* __restrict__ rows,
+                                      int64_t nrows, int64_t n, int64_t k, int64_t ngrp, int64_t group_size,
+                                      uint16_t* __restrict__ out) {
+  const int64_t words_per_row = k / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= nrows * words_per_row) return;
+  const int64_t r = idx / words_per_row, kw = idx - r * words_per_row;
+  const int64_t row = min(max(rows[r], (int64_t)0), n - 1);   // range-checked by the host
+  const uint32_t word = packed[row * words_per_row + kw];
+  uint16_t res[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t g = (kw * 8 + e) / group_size;
+    const float q = (float)((word >> (4 * e)) & 0xFu);
+    const float z = zero ? (float)((zero[(row >> 3) * ngrp + g] >> (4 * (row & 7))) & 0xFu) : 8.0f;
+    res[e] = __builtin_bit_cast(uint16_t, (half_t)((q - z) * scale[row * ngrp + g]));
+  }
+  uint4_t o;
+  o.x = res[0] | ((uint32_t)res[1] << 16);
+  o.y = res[2] | ((uint32_t)res[3] << 16);
+  o.z = res[4] | ((uint32_t)res[5] << 16);
+  o.w = res[6] | ((uint32_t)res[7] << 16);
+  *reinterpret_cast<uint4_t*>(out + idx * 8) = o;
+}
+
 __global__ void w8_decode_kernel(const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t n,
                                  int64_t k, uint16_t* __restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -335,6 +363,27 @@ extern "C" int wq_w4_decode(const int32_t* weight_packed, const float* weight_sc
                      reinterpret_cast<const uint32_t*>(weight_zero_point), g_idx, n, k, num_groups, group_size,
                      weight);
   return check_launch("w4_decode");
+}
+
+extern "C" int wq_w4_decode_rows(const int32_t* weight_packed, const float* weight_scale,
+                                 const int32_t* weight_zero_point, const int64_t* rows, int64_t num_rows, int64_t n,
+                                 int64_t k, int64_t num_groups, int64_t group_size, uint16_t* weight, void* stream) {
+  WQ_REQUIRE(n > 0 && k > 0 && num_groups > 0 && group_size > 0 && num_rows >= 0, WQ_ERR_INVALID_ARGUMENT,
+             "non-positive shape n=%lld k=%lld groups=%lld group_size=%lld rows=%lld", (long long)n, (long long)k,
+             (long long)num_groups, (long long)group_size, (long long)num_rows);
+  WQ_REQUIRE(k % 8 == 0, WQ_ERR_UNSUPPORTED, "decode needs k %% 8 == 0 (k=%lld)", (long long)k);
+  WQ_REQUIRE((k - 1) / group_size < num_groups, WQ_ERR_INVALID_ARGUMENT,
+             "scale has %lld groups but k=%lld, group_size=%lld needs %lld", (long long)num_groups, (long long)k,
+             (long long)group_size, (long long)((k - 1) / group_size + 1));
+  if (num_rows == 0) return WQ_OK;
+  WQ_REQUIRE(weight_packed && weight_scale && rows && weight, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  int64_t blocks;
+  if (launch_1d(num_rows * (k / 8), 256, blocks)) return fail(WQ_ERR_UNSUPPORTED, "decode grid too large");
+  hipLaunchKernelGGL(w4_decode_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint32_t*>(weight_packed), weight_scale,
+                     reinterpret_cast<const uint32_t*>(weight_zero_point), rows, num_rows, n, k, num_groups,
+                     group_size, weight);
+  return check_launch("w4_decode_rows");
 }
 
 extern "C" int wq_w8_decode(const int8_t* qweight, const float* scale, int64_t n, int64_t k, uint16_t* weight,

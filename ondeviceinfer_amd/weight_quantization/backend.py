@@ -75,6 +75,22 @@ def decode_weight(weights: dict, name: str, *, group_size: int = 128) -> torch.T
                              n, k, group_size)
 
 
+def decode_rows(weights: dict, name: str, rows: torch.Tensor) -> torch.Tensor:
+    """fp16 ``[len(rows), K]``: the explicit decode of the sampled rows of one
+    weight, without decoding the rest (``benchmarks/validate_weight_reconstruction.py:20-31``;
+    like the reference, W4 groups are 128 along K).  INT8 channel weights:
+    ``fp16(q[rows] * s[rows])``.  Runs ``wq_w4_decode_rows`` / ``wq_w8_decode``."""
+    prefix = name.removesuffix('.weight')
+    if prefix + '.weight_packed' not in weights:
+        q = weights[name]
+        idx = rows.reshape(-1).to(device=q.device, dtype=torch.int64)
+        return _native.w8_decode(q.index_select(0, idx).contiguous(),
+                                 weights[prefix + '.weight_scale'].index_select(0, idx))
+    n, k = (int(x) for x in weights[prefix + '.weight_shape'].tolist())
+    return _native.w4_decode_rows(weights[prefix + '.weight_packed'], weights[prefix + '.weight_scale'],
+                                  weights.get(prefix + '.weight_zero_point'), rows, n, k, 128)
+
+
 # fused linear -> the prepared projections it concatenates along N, in order
 FUSED_PROJECTIONS = {
     'self_attn.qkv_proj': ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj'),

@@ -102,6 +102,37 @@ def test_decode_random_bit_exact(gpu, use_gidx, sym):
     assert np.array_equal(bits(host(got)), bits(qdq.decode_weight(weights, 'p.weight', group_size=g)))
 
 
+def test_decode_rows_matches_oracle(gpu):
+    """decode_rows (``wq_w4_decode_rows``): the reference KAT
+    (``test_weight_quant_backend.py:38-45``), sampled rows of a 151936-row
+    LM-head-sized weight, the symmetric format and INT8 channel rows, each
+    bit-exact against ``oracle.qdq.decode_rows``."""
+    c = KAT['kat_sampled_rows']
+    scale = np.array(c['weight_scale_f16_bits'], dtype=np.uint16).view(np.float16)
+    w = {'mlp.up_proj.weight_packed': np.full(c['packed_shape'], c['packed_word'], dtype=np.int32),
+         'mlp.up_proj.weight_shape': np.array(c['weight_shape']),
+         'mlp.up_proj.weight_scale': scale,
+         'mlp.up_proj.weight_zero_point': np.array(c['weight_zero_point'], dtype=np.int32)}
+    rows = np.array(c['rows'])
+    got = wq.decode_rows({k: dev(v, gpu) for k, v in w.items()}, c['name'], dev(rows, gpu))
+    assert np.array_equal(bits(host(got)), bits(qdq.decode_rows(w, c['name'], rows)))
+    for sym in (False, True):
+        weights, _ = synth.w4_case(151936, 256, 1, seed=5, symmetric=sym, name='lm_head.weight')
+        rows = np.sort(np.random.default_rng(6).choice(151936, size=333, replace=False))
+        rows[0], rows[-1] = 0, 151935
+        got = wq.decode_rows({k: dev(v, gpu) for k, v in weights.items()}, 'lm_head.weight', dev(rows, gpu))
+        assert got.shape == (333, 256)
+        assert np.array_equal(bits(host(got)), bits(qdq.decode_rows(weights, 'lm_head.weight', rows))), sym
+    _, q, s8, _ = synth.int8_case(40, 256, 1, seed=7)
+    w8 = {'p.weight': q, 'p.weight_scale': s8.reshape(-1, 1)}
+    rows = np.array([39, 0, 17, 17])
+    got = wq.decode_rows({k: dev(v, gpu) for k, v in w8.items()}, 'p.weight', dev(rows, gpu))
+    assert np.array_equal(bits(host(got)), bits(qdq.decode_rows(w8, 'p.weight', rows)))
+    with pytest.raises(IndexError):
+        wq.decode_rows({k: dev(v, gpu) for k, v in weights.items()}, 'lm_head.weight',
+                       torch.tensor([151936], device=gpu))
+
+
 # ------------------------------------------------------------------ W4A16 linear
 
 @pytest.mark.parametrize('m', [1, 2, 15, 16, 17, 33, 64, 65, 128, 300])
