@@ -44,6 +44,24 @@ struct WRegs<GFmt::W8, NT> {
 // LDS slot (16-byte chunk index inside a 256-byte row) of chunk c in row r.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 15); }
 
+// The MT B-fragments of one k-step: fragment mt is row mt*16 + i of the
+// stage, so its address is a per-lane base plus the immediate mt*16 rows
+// (no address arithmetic per read).  Inline asm for the reason given at
+// lds_read16_asm.
+template <int OFF>
+__device__ __forceinline__ uint4_t lds_read16_off(uint32_t a) {
+  uint4_t v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+template <int MT, int MTI = 0>
+__device__ __forceinline__ void lds_read_frags(uint4_t (&b)[MT], uint32_t a) {
+  if constexpr (MTI < MT) {
+    b[MTI] = lds_read16_off<MTI * 16 * kRowBytes>(a);
+    lds_read_frags<MT, MTI + 1>(b, a);
+  }
+}
+
 template <GFmt F, int NT, int MT>
 __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restrict__ x, int M, int K,
                                                          const void* __restrict__ wsrc,
@@ -144,40 +162,40 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
     for (int w = 0; w < 4; ++w) {
       // chunk of this k-step inside the 128-k block, matching the fragment
       const int c = F == GFmt::W4 ? 4 * kb + w : 2 * kb + (w & 1) + 8 * (w >> 1);
+      // row r = mt*16 + i holds chunk c at slot c ^ (r & 15) = c ^ i
       uint4_t b[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int r = mt * 16 + i;
-        b[mt] = lds_read16_asm(stage + r * kRowBytes + swz(r, c) * 16);
-      }
-      half8_t a[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
+      lds_read_frags<MT>(b, (uint32_t)(size_t)((const __attribute__((address_space(3))) uint8_t*)stage) +
+                                (uint32_t)(i * kRowBytes + (c ^ i) * 16));
+      auto dequant = [&](int t) -> half8_t {
         if constexpr (F == GFmt::W4) {
           uint32_t c_lo, c_hi;
           w4_zero_consts((cur.z[t] >> (4 * (i & 7))) & 0xFu, c_lo, c_hi);
           const half2_t s2 = as_h2((uint32_t)cur.s[t] * 0x00010001u);
           const uint32_t word = w == 0 ? cur.w[t].x : w == 1 ? cur.w[t].y : w == 2 ? cur.w[t].z : cur.w[t].w;
-          a[t] = w4_word_to_h8_scaled(word, c_lo, c_hi, s2);
+          return w4_word_to_h8_scaled(word, c_lo, c_hi, s2);
         } else {
-          a[t] = w == 0 ? i8x8_to_h8(cur.a[t].x, cur.a[t].y)
+          return w == 0 ? i8x8_to_h8(cur.a[t].x, cur.a[t].y)
                : w == 1 ? i8x8_to_h8(cur.a[t].z, cur.a[t].w)
                : w == 2 ? i8x8_to_h8(cur.b[t].x, cur.b[t].y)
                         : i8x8_to_h8(cur.b[t].z, cur.b[t].w);
         }
-      }
-      // The dequantization above overlaps the reads; the first half of the
-      // m-subtiles runs while the second half is still in flight.
+      };
+      // Tile-outer order: tile t+1 is dequantized (VALU) while tile t's MT
+      // MFMAs run.  Tile 0's first half of m-subtiles starts while the second
+      // half of the fragments is still in flight.
+      half8_t a = dequant(0);
       lds_wait_first_half<MT>(b);
 #pragma unroll
-      for (int mt = 0; mt < MT / 2; ++mt)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], __builtin_bit_cast(half8_t, b[mt]), acc[t][mt]);
+      for (int mt = 0; mt < MT / 2; ++mt) acc[0][mt] = mfma16(a, __builtin_bit_cast(half8_t, b[mt]), acc[0][mt]);
       lds_wait_rest<MT>(b);
 #pragma unroll
-      for (int mt = MT / 2; mt < MT; ++mt)
+      for (int t = 0; t < NT; ++t) {
+        const half8_t a_next = t + 1 < NT ? dequant(t + 1) : a;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma16(a[t], __builtin_bit_cast(half8_t, b[mt]), acc[t][mt]);
+        for (int mt = t == 0 ? MT / 2 : 0; mt < MT; ++mt)
+          acc[t][mt] = mfma16(a, __builtin_bit_cast(half8_t, b[mt]), acc[t][mt]);
+        a = a_next;
+      }
     }
     if (more) cur = nxt;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's part of the next stage landed
