@@ -175,6 +175,19 @@ int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweig
                     const uint16_t* scale, int64_t n, const uint16_t* bias, uint16_t* y,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* The INT8 counterpart of wq_w4a16_decode_fused: one decode-token (M = 1)
+ * INT8 x fp16 linear on the stored [n, k] weight with the fp16 row scale,
+ * with the same x_mode / residual / sumsq_out fusions (n % 16 == 0,
+ * k % 128 == 0; x, qweight, y, norm_weight and sumsq_in 16-byte aligned,
+ * residual 8-byte).  y = residual + fp16(scale[n] * (x . q[n])) when residual
+ * is given.  Workspace as for wq_w8a16_linear at m = 1.  Replaces, in the
+ * INT8 weight-only decoder layer, the same rms_norm / residual / SiLU*up ops
+ * around int8_weight_only_linear (quantized_model.py:146-227, :101-121). */
+int wq_w8a16_decode_fused(const uint16_t* x, int64_t k, const int8_t* qweight, const uint16_t* scale, int64_t n,
+                          int32_t x_mode, const uint16_t* norm_weight, const float* sumsq_in, int64_t sumsq_count,
+                          float eps, const uint16_t* residual, float* sumsq_out, uint16_t* y, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* Symmetric per-output-channel INT8 quantizer: weight fp32 [n, k] ->
  * qweight int8 [n, k] + fp16 scale [n] (absmax/127, zero rows scale 1,
  * underflowing scales -> smallest fp16 subnormal, the stored scale divides,

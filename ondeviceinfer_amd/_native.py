@@ -52,6 +52,8 @@ _SIGNATURES = {
     'wq_w4a16_linear_noalloc': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P],
     'wq_w4a16_decode_fused': [_P, _I64, _P, _P, _I64, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P,
                               _P, _P, ctypes.c_size_t, _P],
+    'wq_w8a16_decode_fused': [_P, _I64, _P, _P, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P, _P, _P,
+                              ctypes.c_size_t, _P],
     'wq_w8_decode': [_P, _P, _I64, _I64, _P, _P],
     'wq_w8a16_workspace_size': [_I64, _I64, _I64, _SIZE_P],
     'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
@@ -317,15 +319,8 @@ def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: in
 X_PLAIN, X_RMSNORM, X_SILU_MUL = 0, 1, 2
 
 
-def w4a16_decode_fused(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: int, group_size: int, *,
-                       x_mode: int = X_PLAIN, norm_weight: torch.Tensor | None = None,
-                       sumsq_in: torch.Tensor | None = None, eps: float = 1e-6,
-                       residual: torch.Tensor | None = None, sumsq_out: torch.Tensor | None = None,
-                       out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """One decode-token W4A16 linear with the fused prologue/epilogue of
-    ``wq_w4a16_decode_fused`` (x_mode ``X_PLAIN`` / ``X_RMSNORM`` /
-    ``X_SILU_MUL``; ``residual`` added in fp16; per-tile ``sumsq_out``)."""
-    device = _require_gpu(x, tiles, meta, norm_weight, sumsq_in, residual, sumsq_out, out, workspace)
+def _decode_fused_args(x, n, x_mode, norm_weight, sumsq_in, residual, sumsq_out, out, device):
+    """Checks shared by the fused decode linears; returns (k, out)."""
     if x.dtype != torch.float16 or not x.is_contiguous():
         raise TypeError('x must be a contiguous float16 tensor')
     k = x.numel() // 2 if x_mode == X_SILU_MUL else x.numel()
@@ -342,11 +337,54 @@ def w4a16_decode_fused(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor,
         out = torch.empty((1, n), dtype=torch.float16, device=device)
     elif out.dtype != torch.float16 or out.numel() != n or not out.is_contiguous():
         raise ValueError(f'out must be contiguous float16 with {n} elements')
+    return k, out
+
+
+def _ws_args(workspace):
+    if workspace is None:
+        return None, 0
+    return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+
+
+def w4a16_decode_fused(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: int, group_size: int, *,
+                       x_mode: int = X_PLAIN, norm_weight: torch.Tensor | None = None,
+                       sumsq_in: torch.Tensor | None = None, eps: float = 1e-6,
+                       residual: torch.Tensor | None = None, sumsq_out: torch.Tensor | None = None,
+                       out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode-token W4A16 linear with the fused prologue/epilogue of
+    ``wq_w4a16_decode_fused`` (x_mode ``X_PLAIN`` / ``X_RMSNORM`` /
+    ``X_SILU_MUL``; ``residual`` added in fp16; per-tile ``sumsq_out``)."""
+    device = _require_gpu(x, tiles, meta, norm_weight, sumsq_in, residual, sumsq_out, out, workspace)
+    k, out = _decode_fused_args(x, n, x_mode, norm_weight, sumsq_in, residual, sumsq_out, out, device)
     if workspace is None:
         workspace = shared_workspace(device, w4a16_workspace_size(1, n, k, group_size), ('w4a16', 1, n, k, group_size))
-    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
-                                                             workspace.numel() * workspace.element_size())
+    ws_ptr, ws_bytes = _ws_args(workspace)
     _call('wq_w4a16_decode_fused', _ptr(x), k, _ptr(tiles), _ptr(meta), n, group_size, x_mode, _ptr(norm_weight),
+          _ptr(sumsq_in), 0 if sumsq_in is None else sumsq_in.numel(), float(eps), _ptr(residual), _ptr(sumsq_out),
+          _ptr(out), ws_ptr, ws_bytes, _stream(device))
+    return out
+
+
+def w8a16_decode_fused(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, *,
+                       x_mode: int = X_PLAIN, norm_weight: torch.Tensor | None = None,
+                       sumsq_in: torch.Tensor | None = None, eps: float = 1e-6,
+                       residual: torch.Tensor | None = None, sumsq_out: torch.Tensor | None = None,
+                       out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The INT8 (row-major [n, k] weight, fp16 row scale) counterpart of
+    ``w4a16_decode_fused`` (``wq_w8a16_decode_fused``)."""
+    device = _require_gpu(x, qweight, scale, norm_weight, sumsq_in, residual, sumsq_out, out, workspace)
+    if qweight.dtype != torch.int8 or qweight.dim() != 2 or not qweight.is_contiguous():
+        raise TypeError('qweight must be a contiguous 2-D INT8 tensor')
+    n, kq = qweight.shape
+    if scale.dtype != torch.float16 or scale.numel() != n or not scale.is_contiguous():
+        raise ValueError(f'scale must be contiguous float16 with {n} entries')
+    k, out = _decode_fused_args(x, n, x_mode, norm_weight, sumsq_in, residual, sumsq_out, out, device)
+    if k != kq:
+        raise ValueError(f'input has {k} features, expected {kq}')
+    if workspace is None:
+        workspace = shared_workspace(device, w8a16_workspace_size(1, n, k), ('w8a16', 1, n, k))
+    ws_ptr, ws_bytes = _ws_args(workspace)
+    _call('wq_w8a16_decode_fused', _ptr(x), k, _ptr(qweight), _ptr(scale), n, x_mode, _ptr(norm_weight),
           _ptr(sumsq_in), 0 if sumsq_in is None else sumsq_in.numel(), float(eps), _ptr(residual), _ptr(sumsq_out),
           _ptr(out), ws_ptr, ws_bytes, _stream(device))
     return out

@@ -33,6 +33,10 @@ int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uin
                          int x_mode, const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
                          const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
                          hipStream_t s);
+int launch_w8_gemv_fused(const half_t* x, int K, const int8_t* q, const half_t* scale, int N, int x_mode,
+                         const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
+                         const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
+                         hipStream_t s);
 
 // Largest M served by the MFMA GEMV (4 chunks of 16 activation rows).
 constexpr int64_t kSkinnyMaxM = 64;
@@ -133,6 +137,27 @@ extern "C" int wq_w4a16_decode_fused(const uint16_t* x, int64_t k, const void* t
              "x, tiles, y, norm_weight and sumsq_in must be 16-byte aligned, meta and residual 8-byte");
   return launch_w4_gemv_fused(reinterpret_cast<const half_t*>(x), (int)k, reinterpret_cast<const uint4_t*>(tiles),
                               reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, x_mode,
+                              reinterpret_cast<const half_t*>(norm_weight), sumsq_in, (int)sumsq_count, eps,
+                              reinterpret_cast<const half_t*>(residual), sumsq_out, reinterpret_cast<half_t*>(y),
+                              workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int wq_w8a16_decode_fused(const uint16_t* x, int64_t k, const int8_t* qweight, const uint16_t* scale,
+                                     int64_t n, int32_t x_mode, const uint16_t* norm_weight, const float* sumsq_in,
+                                     int64_t sumsq_count, float eps, const uint16_t* residual, float* sumsq_out,
+                                     uint16_t* y, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int st = linear_shape_check(1, n, k)) return st;
+  WQ_REQUIRE(n % 16 == 0 && k % kW8BlockK == 0, WQ_ERR_UNSUPPORTED,
+             "fused decode linear needs n %% 16 == 0 and k %% 128 == 0 (n=%lld k=%lld)", (long long)n, (long long)k);
+  WQ_REQUIRE(x_mode >= 0 && x_mode <= 2, WQ_ERR_INVALID_ARGUMENT, "x_mode must be 0 (plain), 1 (rmsnorm) or 2 (silu_mul)");
+  WQ_REQUIRE(x && qweight && scale && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(x_mode != 1 || (norm_weight && sumsq_in && sumsq_count > 0 && sumsq_count <= 512),
+             WQ_ERR_INVALID_ARGUMENT, "rmsnorm mode needs norm_weight, sumsq_in and 0 < sumsq_count <= 512");
+  WQ_REQUIRE(aligned16(x) && aligned16(qweight) && aligned16(y) && aligned16(norm_weight) && aligned16(sumsq_in) &&
+                 (reinterpret_cast<uintptr_t>(residual) & 7u) == 0,
+             WQ_ERR_INVALID_ARGUMENT, "x, qweight, y, norm_weight and sumsq_in must be 16-byte aligned, residual 8-byte");
+  return launch_w8_gemv_fused(reinterpret_cast<const half_t*>(x), (int)k, qweight,
+                              reinterpret_cast<const half_t*>(scale), (int)n, x_mode,
                               reinterpret_cast<const half_t*>(norm_weight), sumsq_in, (int)sumsq_count, eps,
                               reinterpret_cast<const half_t*>(residual), sumsq_out, reinterpret_cast<half_t*>(y),
                               workspace, workspace_bytes, as_stream(stream));

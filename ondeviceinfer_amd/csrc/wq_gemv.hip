@@ -291,7 +291,7 @@ __device__ __forceinline__ int blk_kcol(int kb, int w) {
   return F == WFmt::W4 ? kb * 32 + 8 * w : kb * 16 + 8 * (w & 1) + 64 * (w >> 1);
 }
 
-// Decode-step fusions of the flat GEMV (M = 1, W4): how x is formed while it
+// Decode-step fusions of the flat GEMV (M = 1, W4 and INT8): how x is formed while it
 // is staged, and the residual / sum-of-squares epilogue.
 enum class XMode {
   Plain,     // x as given
@@ -388,11 +388,11 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
       sq[u] = reinterpret_cast<const float4_t*>(fz.sumsq_in)[max(min(lane + 64 * u, fz.sumsq_count / 4 - 1), 0)];
     sqt = fz.sumsq_in[min((fz.sumsq_count & ~3) + (lane & 3), fz.sumsq_count - 1)];
   }
-  // The fused residual (W4, M = 1; wave 0 stores the tile) is fetched now so
+  // The fused residual (M = 1; wave 0 stores the tile) is fetched now so
   // that its latency is not added after the reduction (for NB <= 8, where the
   // two registers are free).  Every split reads it before it counts in, so
   // an aliased y still holds the old value here.
-  constexpr bool kEarlyResidual = F == WFmt::W4 && NB <= 8;
+  constexpr bool kEarlyResidual = NB <= 8;
   const bool has_x = i < M;
   const int n0 = tile * 16 + 4 * kb;
   half4_t res = {};
@@ -533,37 +533,44 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
     if (lane == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (has_x) {
+    // Lane (i, kb) holds outputs n0 .. n0 + 3 of row i.  W4 applies the
+    // group scales per block; INT8 applies the row scale (and bias) here.
+    half4_t o;
     if constexpr (F == WFmt::W4) {
-      half4_t o;
 #pragma unroll
       for (int v = 0; v < 4; ++v) o[v] = (half_t)sum[v];
-      if (n0 < N) {
-        // Fused residual (M = 1): y = residual + fp16(x.W^T), as the
-        // reference adds the rounded projection to the fp16 residual.
-        if (fz.residual) o = (kEarlyResidual ? res : *reinterpret_cast<const half4_t*>(fz.residual + n0)) + o;
-        *reinterpret_cast<half4_t*>(y + (size_t)i * N + n0) = o;
-      }
-      if (fz.sumsq_out) {
-        // Lanes 0, 16, 32, 48 hold the tile's 16 outputs (M = 1).
-        float q = 0.f;
-        if (n0 < N) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) q += (float)o[v] * (float)o[v];
-        }
-        q = (lane_f(q, 0) + lane_f(q, 16)) + (lane_f(q, 32) + lane_f(q, 48));
-        if (lane == 0) fz.sumsq_out[tile] = q;
-      }
     } else {
       const half_t* scale = reinterpret_cast<const half_t*>(wmeta);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int n = n0 + v;
-        if (n < N) {
-          float r = sum[v] * (float)scale[n];
-          if (bias) r += (float)bias[n];
-          y[(size_t)i * N + n] = (half_t)r;
-        }
+        const int n = min(n0 + v, N - 1);
+        float r = sum[v] * (float)scale[n];
+        if (bias) r += (float)bias[n];
+        o[v] = (half_t)r;
       }
+    }
+    // W4 rows come in whole 16-row tiles; INT8 stores a quad at once when
+    // every row of y keeps 8-byte alignment, else element-wise.
+    const bool quad = F == WFmt::W4 || ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0);
+    if (quad && n0 < N) {
+      // Fused residual (M = 1): y = residual + fp16(x.W^T), as the
+      // reference adds the rounded projection to the fp16 residual.
+      if (fz.residual) o = (kEarlyResidual ? res : *reinterpret_cast<const half4_t*>(fz.residual + n0)) + o;
+      *reinterpret_cast<half4_t*>(y + (size_t)i * N + n0) = o;
+    } else if (!quad) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (n0 + v < N) y[(size_t)i * N + n0 + v] = o[v];
+    }
+    if (fz.sumsq_out) {
+      // Lanes 0, 16, 32, 48 hold the tile's 16 outputs (M = 1).
+      float q = 0.f;
+      if (n0 < N) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) q += (float)o[v] * (float)o[v];
+      }
+      q = (lane_f(q, 0) + lane_f(q, 16)) + (lane_f(q, 32) + lane_f(q, 48));
+      if (lane == 0) fz.sumsq_out[tile] = q;
     }
   }
 }
@@ -762,10 +769,8 @@ int launch_gemv_flat(const half_t* x, int M, int K, const void* w, const void* m
     p = plan_flat<F>(ntile, nblk, false);
   const int nb = (nblk / p.split) / p.ksw;
   if (nb < 1 || nb > kFlatMaxNB) return kNotApplicable;
-  if constexpr (F == WFmt::W4) {
-    if (xm == XMode::RmsNorm) return launch_flat_nb<1, F, XMode::RmsNorm>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
-    if (xm == XMode::SiluMul) return launch_flat_nb<1, F, XMode::SiluMul>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
-  }
+  if (xm == XMode::RmsNorm) return launch_flat_nb<1, F, XMode::RmsNorm>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
+  if (xm == XMode::SiluMul) return launch_flat_nb<1, F, XMode::SiluMul>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
   if (M == 1) return launch_flat_nb<1, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
   return launch_flat_nb<4, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
 }
@@ -789,6 +794,18 @@ int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uin
   const XMode xm = x_mode == 1 ? XMode::RmsNorm : x_mode == 2 ? XMode::SiluMul : XMode::Plain;
   const int rc = launch_gemv_flat<WFmt::W4>(x, 1, K, tiles, meta, nullptr, N, __builtin_ctz(bpg), y, ws, ws_bytes, s,
                                             xm, fz);
+  if (rc == kNotApplicable)
+    return fail(WQ_ERR_UNSUPPORTED, "fused decode linear: this k is beyond the decode kernel's blocks per wave");
+  return rc;
+}
+
+int launch_w8_gemv_fused(const half_t* x, int K, const int8_t* q, const half_t* scale, int N, int x_mode,
+                         const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
+                         const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
+                         hipStream_t s) {
+  const FuseArgs fz{norm_w, sumsq_in, sumsq_count, eps, residual, sumsq_out};
+  const XMode xm = x_mode == 1 ? XMode::RmsNorm : x_mode == 2 ? XMode::SiluMul : XMode::Plain;
+  const int rc = launch_gemv_flat<WFmt::W8>(x, 1, K, q, scale, nullptr, N, 0, y, ws, ws_bytes, s, xm, fz);
   if (rc == kNotApplicable)
     return fail(WQ_ERR_UNSUPPORTED, "fused decode linear: this k is beyond the decode kernel's blocks per wave");
   return rc;

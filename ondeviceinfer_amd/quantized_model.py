@@ -215,9 +215,10 @@ class DecodeStepGraph:
     linear (RMSNorm in its prologue), attention (q/k norm, RoPE, KV append,
     GQA softmax, chunk merge), o linear (+ residual), fused gate_up linear
     (RMSNorm prologue), down linear (SiLU*up prologue, + residual)] -> final
-    norm -> fp16 LM head with the greedy token picked in the same pass.  W8
-    weights take the same steps with the norms, residual adds and SiLU*up as
-    separate kernels.  Inputs are the token id and the position (device
+    norm -> fp16 LM head with the greedy token picked in the same pass, for
+    W4 and INT8 (W8A16) weights alike; other formats (W8A8) take the same
+    steps with the norms, residual adds and SiLU*up as separate kernels.
+    Inputs are the token id and the position (device
     scalars); every launch is a HIP kernel of this library except the
     embedding gather (torch), and the LM head falls back to torch's GEMM
     when the hidden size is not a multiple of 512."""
@@ -259,10 +260,14 @@ class DecodeStepGraph:
                     raise ValueError(f'decode graph needs prepared {name}')
         self.embed = model.device_embedding()
         self.lm_head_t = model.lm_head.t()
-        from .weight_quantization.backend import PreparedW4
+        from .weight_quantization.backend import PreparedW4, PreparedW8
         names = ('self_attn.qkv_proj', 'self_attn.o_proj', 'mlp.gate_up_proj', 'mlp.down_proj')
-        self.fused = all(isinstance(w[p + '._prepared'], PreparedW4) for w in self.layers for p in names) and \
-            hidden % 16 == 0
+        prepared = [w[p + '._prepared'] for w in self.layers for p in names]
+        # The fused decode linears take one weight format per step; INT8 also
+        # needs k in whole 128-k blocks.
+        self.fused = hidden % 16 == 0 and all(p.n % 16 == 0 for p in prepared) and (
+            all(isinstance(p, PreparedW4) for p in prepared) or
+            all(isinstance(p, PreparedW8) and p.k % 128 == 0 for p in prepared))
         self.sumsq_o = torch.zeros(hidden // 16, dtype=torch.float32, device=dev)
         self.sumsq_down = torch.zeros(hidden // 16, dtype=torch.float32, device=dev)
         # One eager step loads every code object and the GEMM's handles, then
@@ -285,13 +290,21 @@ class DecodeStepGraph:
         else:
             self._step_unfused()
 
+    @staticmethod
+    def _fused_linear(x: Tensor, p, **kw) -> None:
+        if hasattr(p, 'tiles'):
+            _native.w4a16_decode_fused(x, p.tiles, p.meta, p.n, p.group_size, workspace=p.workspace, **kw)
+        else:
+            _native.w8a16_decode_fused(x, p.qweight, p.scale, **kw)
+
     def _step_fused(self) -> None:
-        """W4 weights: the RMSNorms, residual adds and SiLU*up ride inside the
-        decode linears (wq_w4a16_decode_fused): per layer one QKV linear, the
-        attention, and the o, gate_up and down linears."""
+        """The RMSNorms, residual adds and SiLU*up ride inside the decode
+        linears (wq_w4a16_decode_fused / wq_w8a16_decode_fused): per layer one
+        QKV linear, the attention, and the o, gate_up and down linears."""
         cfg = self.model.config
         eps = cfg.rms_norm_eps
         nat = _native
+        lin = self._fused_linear
         torch.index_select(self.embed, 0, self.token, out=self.hidden)
         hid = self.hidden.view(-1)
         for idx, w in enumerate(self.layers):
@@ -299,24 +312,19 @@ class DecodeStepGraph:
             gu_p, dn_p = w[GATE_UP_FUSED.removesuffix('.weight') + '._prepared'], w['mlp.down_proj._prepared']
             if idx == 0:
                 nat.add_rmsnorm(self.hidden, w['input_layernorm.weight'], eps, out=self.states)
-                nat.w4a16_decode_fused(self.states.view(-1), qkv_p.tiles, qkv_p.meta, qkv_p.n, qkv_p.group_size,
-                                       out=self.qkv, workspace=qkv_p.workspace)
+                lin(self.states.view(-1), qkv_p, out=self.qkv)
             else:
-                nat.w4a16_decode_fused(hid, qkv_p.tiles, qkv_p.meta, qkv_p.n, qkv_p.group_size,
-                                       x_mode=nat.X_RMSNORM, norm_weight=w['input_layernorm.weight'],
-                                       sumsq_in=self.sumsq_down, eps=eps, out=self.qkv, workspace=qkv_p.workspace)
+                lin(hid, qkv_p, x_mode=nat.X_RMSNORM, norm_weight=w['input_layernorm.weight'],
+                    sumsq_in=self.sumsq_down, eps=eps, out=self.qkv)
             nat.decode_attention(self.qkv.view(-1), cfg.num_attention_heads, cfg.num_key_value_heads,
                                  w['self_attn.q_norm.weight'], w['self_attn.k_norm.weight'], eps, self.cos,
                                  self.sin, self.position, self.kc[idx], self.vc[idx], self.scale, out=self.attn,
                                  workspace=self.attn_ws)
-            nat.w4a16_decode_fused(self.attn, o_p.tiles, o_p.meta, o_p.n, o_p.group_size, residual=hid,
-                                   sumsq_out=self.sumsq_o, out=hid, workspace=o_p.workspace)
-            nat.w4a16_decode_fused(hid, gu_p.tiles, gu_p.meta, gu_p.n, gu_p.group_size, x_mode=nat.X_RMSNORM,
-                                   norm_weight=w['post_attention_layernorm.weight'], sumsq_in=self.sumsq_o, eps=eps,
-                                   out=self.gate_up, workspace=gu_p.workspace)
-            nat.w4a16_decode_fused(self.gate_up.view(-1), dn_p.tiles, dn_p.meta, dn_p.n, dn_p.group_size,
-                                   x_mode=nat.X_SILU_MUL, residual=hid, sumsq_out=self.sumsq_down, out=hid,
-                                   workspace=dn_p.workspace)
+            lin(self.attn, o_p, residual=hid, sumsq_out=self.sumsq_o, out=hid)
+            lin(hid, gu_p, x_mode=nat.X_RMSNORM, norm_weight=w['post_attention_layernorm.weight'],
+                sumsq_in=self.sumsq_o, eps=eps, out=self.gate_up)
+            lin(self.gate_up.view(-1), dn_p, x_mode=nat.X_SILU_MUL, residual=hid, sumsq_out=self.sumsq_down,
+                out=hid)
         nat.add_rmsnorm(self.hidden, self.model.final_norm, eps, out=self.states)
         self._lm_head()
 

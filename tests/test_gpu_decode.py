@@ -297,6 +297,53 @@ def test_w4a16_decode_fused_matches_oracle(nat, k, n, mode):
     assert np.allclose(ss.cpu().numpy(), (g64 ** 2).reshape(-1, 16).sum(-1), rtol=1e-5, atol=1e-3)
 
 
+@pytest.mark.parametrize('k,n,mode', [(5120, 7168, 1), (5120, 5120, 0), (17408, 5120, 2), (5120, 34816, 1),
+                                      (512, 1024, 2), (256, 512, 0)])
+def test_w8a16_decode_fused_matches_oracle(nat, k, n, mode):
+    """wq_w8a16_decode_fused (INT8 weight, fp16 row scale) in every mode
+    against the oracle: fp16(q * s) weights (the reference's
+    int8_weight_only_linear), its RMSNorm / SiLU*up, the fp16 residual add and
+    the per-tile sums of squares."""
+    from oracle import synth
+    print(f'[w8 decode_fused] k={k} n={n} mode={mode}', flush=True)
+    _, q, s, _ = synth.int8_case(n, k, 1, seed=k + n + mode)
+    rng = np.random.default_rng(mode + 10)
+    res = (rng.standard_normal(n) * 4).astype(np.float16)
+    if mode == 2:
+        xin = (rng.standard_normal(2 * k) * 2).astype(np.float16)
+        x_eff = qwen3.swiglu(xin[:k], xin[k:])
+        kw = {}
+    elif mode == 1:
+        xin = (rng.standard_normal(k) * 3).astype(np.float16)
+        nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float16)
+        x_eff = qwen3.rms_norm(xin, nw, 1e-6)
+        parts = (xin.astype(np.float32) ** 2).reshape(-1, 16).sum(-1).astype(np.float32)
+        kw = {'norm_weight': torch.from_numpy(nw).cuda(), 'sumsq_in': torch.from_numpy(parts).cuda()}
+    else:
+        xin = rng.standard_normal(k).astype(np.float16)
+        x_eff = xin
+        kw = {}
+    y_lin = qdq.linear_fp32(x_eff[None], qdq.dequantize_linear_weight(q, s))[0]
+    expect = (res + y_lin).astype(np.float16)
+    hid = torch.from_numpy(res.copy()).cuda()
+    ss = torch.zeros(n // 16, dtype=torch.float32, device='cuda')
+    out = nat.w8a16_decode_fused(torch.from_numpy(xin).cuda(), torch.from_numpy(q).cuda(),
+                                 torch.from_numpy(s).cuda(), x_mode=mode, residual=hid, sumsq_out=ss, out=hid, **kw)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert out.data_ptr() == hid.data_ptr()
+    m = qdq.parity_metrics(got.astype(np.float32) - res, expect.astype(np.float32) - res)
+    assert qdq.parity_ok(m), m
+    g64 = got.astype(np.float64)
+    assert np.allclose(ss.cpu().numpy(), (g64 ** 2).reshape(-1, 16).sum(-1), rtol=1e-5, atol=1e-3)
+    # Without the fusions the entry point is the plain INT8 linear, bit for bit.
+    if mode == 0:
+        xt = torch.from_numpy(xin).cuda()
+        plain = nat.w8a16_decode_fused(xt, torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda())
+        ref = nat.w8a16_linear(xt[None], torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda())
+        assert torch.equal(plain.view(-1), ref.view(-1))
+
+
 # ------------------------------------------------------------------ LM head + greedy token
 
 def _lm_case(vocab, k, seed):
