@@ -145,6 +145,118 @@ __global__ __launch_bounds__(64 * KSW) void w4_skinny_kernel(const half_t* __res
   });
 }
 
+// W4A16, M <= 16*MC, as a continuous load ring: each wave keeps its next U
+// k blocks (the TPW tiles' weights and scale/zero records and the MC
+// activation fragments) in flight and refills a slot as soon as it is
+// consumed.  Every load goes through a buffer resource whose range ends at
+// the wave's last block (weights), the tile's last group (records) or row M
+// (activations), so loads past an end are unconditional and read zeros
+// without touching memory; the per-block math and its order are those of
+// w4_skinny_kernel.  Used for K <= 2^25, where the 32-bit lane offsets
+// (up to 15 rows of x plus K) and the per-tile weight ranges fit.
+template <int MC, int TPW>
+struct SkinnySlot {
+  uint4_t w[TPW];
+  uint2_t sc[TPW];
+  uint32_t zw[TPW];
+  half8_t xv[MC][4];
+};
+
+template <int MC, int TPW, int KSW, int U>
+__global__ __launch_bounds__(64 * KSW) void w4_skinny_ring_kernel(const half_t* __restrict__ x, int M, int K,
+                                                                  const uint4_t* __restrict__ tiles,
+                                                                  const uint8_t* __restrict__ meta, int N, int G,
+                                                                  half_t* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15, kb = lane >> 4;
+  const int ntile = (N + 15) >> 4;
+  const int nblk = K / kW4BlockK, ngrp = K / G, bpg = G / kW4BlockK;
+  const int b_lo = (wave * nblk) / KSW, nb = ((wave + 1) * nblk) / KSW - b_lo;
+
+  __amdgpu_buffer_rsrc_t rw[TPW], rm[TPW], rx[MC];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = min((int)blockIdx.x * TPW + t, ntile - 1);
+    rw[t] = buf_rsrc(tiles + ((size_t)tile * nblk + b_lo) * 64, (int64_t)nb * 1024);
+    rm[t] = buf_rsrc(meta + (size_t)tile * ngrp * kW4MetaBytes, (int64_t)ngrp * kW4MetaBytes);
+  }
+#pragma unroll
+  for (int mc = 0; mc < MC; ++mc)
+    rx[mc] = buf_rsrc(x + (size_t)mc * 16 * K, (int64_t)min(max(M - mc * 16, 0), 16) * K * 2);
+  const uint32_t xo = (uint32_t)((i * K + kb * 32) * 2);
+
+  auto load = [&](SkinnySlot<MC, TPW>& s, int r) {
+    // r: block index relative to b_lo; past the wave's range every load is out of bounds.
+    const bool in = r < nb;
+    const uint32_t wo = (uint32_t)r * 1024;
+    const uint32_t mo = in ? (uint32_t)(((b_lo + r) / bpg) * kW4MetaBytes) : 0x7ffff000u;
+    const uint32_t xs = in ? (uint32_t)(b_lo + r) * kW4BlockK * 2 : 0x7ffff000u;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      s.w[t] = __builtin_amdgcn_raw_buffer_load_b128(rw[t], (uint32_t)lane * 16, wo, kNtPolicy);
+      s.sc[t] = __builtin_bit_cast(uint2_t, __builtin_amdgcn_raw_buffer_load_b64(rm[t], (uint32_t)kb * 8, mo, 0));
+      s.zw[t] = __builtin_amdgcn_raw_buffer_load_b32(rm[t], 32 + (uint32_t)(i >> 3) * 4, mo, 0);
+    }
+#pragma unroll
+    for (int mc = 0; mc < MC; ++mc)
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        s.xv[mc][w] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx[mc], xo + 16 * w, xs, 0));
+  };
+
+  float4_t acc[MC][TPW];
+#pragma unroll
+  for (int mc = 0; mc < MC; ++mc)
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) acc[mc][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](const SkinnySlot<MC, TPW>& s) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      uint32_t c_lo, c_hi;
+      w4_zero_consts((s.zw[t] >> (4 * (i & 7))) & 0xFu, c_lo, c_hi);
+      float4_t cg[MC];
+#pragma unroll
+      for (int mc = 0; mc < MC; ++mc) cg[mc] = float4_t{0.f, 0.f, 0.f, 0.f};
+      const uint32_t words[4] = {s.w[t].x, s.w[t].y, s.w[t].z, s.w[t].w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const half8_t a = w4_word_to_h8(words[w], c_lo, c_hi);
+#pragma unroll
+        for (int mc = 0; mc < MC; ++mc) cg[mc] = mfma16(a, s.xv[mc][w], cg[mc]);
+      }
+      const half4_t s4 = __builtin_bit_cast(half4_t, s.sc[t]);
+#pragma unroll
+      for (int mc = 0; mc < MC; ++mc)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[mc][t][v] += (float)s4[v] * cg[mc][v];
+    }
+  };
+
+  SkinnySlot<MC, TPW> ring[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) load(ring[u], u);
+  for (int r0 = 0; r0 < nb; r0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (r0 + u < nb) consume(ring[u]);
+      load(ring[u], r0 + u + U);
+    }
+  }
+
+  skinny_epilogue<MC, TPW, KSW>(acc, lane, wave, [&](int mc, int t, int l, float4_t s) {
+    const int m = mc * 16 + (l & 15);
+    const int t_out = (int)blockIdx.x * TPW + t;
+    const int n0 = t_out * 16 + 4 * (l >> 4);
+    if (m < M && t_out < ntile && n0 < N) {
+      half4_t o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = (half_t)s[v];
+      *reinterpret_cast<half4_t*>(y + (size_t)m * N + n0) = o;
+    }
+  });
+}
+
 // INT8 x fp16, M <= 16*MC, weights [N, K] row-major int8, fp16 row scale.
 // Lane (i, kb) of block blk reads row 16t+i at k = 128*blk + 16*kb + [0,16)
 // and 128*blk + 64 + 16*kb + [0,16); each 16 B feeds two MFMA k-steps.
@@ -632,13 +744,31 @@ SkinnyCfg pick_skinny(int ntile, int nblk, int mc, bool w4) {
   return c;
 }
 
+// The load ring pays where a wave streams many blocks per tile group: wide N
+// (>= 1024 tiles, four tiles per wave) or long K at M <= 16, and at
+// 33 <= M <= 48.  The batch form stays ahead on the fused QKV shape at
+// M <= 16, at 17 <= M <= 32 and at M > 48 (MI355X, same box: gate_up M = 8
+// 31.5 -> 26.9 us, lm_head M = 8 98.6 -> 84.4 us, 17408->5120 M = 8
+// 21.4 -> 19.8 us, gate_up M = 33 67.7 -> 54.0 us; QKV M = 8 9.0 against
+// 9.5 us, gate_up M = 32 46.6 against 49.9 us, lm_head M = 64 235 against
+// 238 us).  Both give the same bits.
+bool skinny_use_ring(int mc, int ntile, int nblk, int K) {
+  if (K > (1 << 25)) return false;   // the ring's lane offsets are 32-bit
+  if (mc == 1) return ntile >= 1024 || nblk >= 64;
+  return mc == 3;
+}
+
 template <int MC, int TPW, int KSW>
 int launch_w4_skinny_cfg(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                          half_t* y, hipStream_t s) {
   const int ntile = (N + 15) / 16;
   const unsigned grid = (unsigned)((ntile + TPW - 1) / TPW);
-  hipLaunchKernelGGL((w4_skinny_kernel<MC, TPW, KSW, skinny_unroll<MC>()>), dim3(grid), dim3(64 * KSW), 0, s, x, M, K, tiles, meta, N,
-                     G, y);
+  if (skinny_use_ring(MC, ntile, K / kW4BlockK, K))
+    hipLaunchKernelGGL((w4_skinny_ring_kernel<MC, TPW, KSW, 2>), dim3(grid), dim3(64 * KSW), 0, s, x, M, K, tiles,
+                       meta, N, G, y);
+  else
+    hipLaunchKernelGGL((w4_skinny_kernel<MC, TPW, KSW, skinny_unroll<MC>()>), dim3(grid), dim3(64 * KSW), 0, s, x, M,
+                       K, tiles, meta, N, G, y);
   return check_launch("w4_skinny");
 }
 

@@ -156,6 +156,20 @@ def test_w4a16_skinny_four_tiles_per_wave(gpu, m):
     check_parity(host(y), qdq.qdq_linear(x, weights, name), f'w4 skinny m={m} n=16400')
 
 
+@pytest.mark.parametrize('m,g,sym', [(5, 128, False), (8, 256, False), (16, 128, True), (33, 128, False),
+                                     (64, 256, True)])
+def test_w4a16_skinny_load_ring_long_k(gpu, m, g, sym):
+    """The skinny load ring on a narrow, long-K shape (66 blocks over the
+    waves of a k-split, 63 tiles, the last one partial): groups of 128 and
+    256, symmetric and with zero points, M = 5 .. 64; every output against
+    the oracle."""
+    name = 'p.weight'
+    weights, x = synth.w4_case(1000, 8448, m, seed=m + g, group_size=g, symmetric=sym, name=name)
+    backend, layer = prepared_w4(weights, name, gpu, group_size=g)
+    y = backend.linear(dev(x, gpu), layer, name)
+    check_parity(host(y), qdq.qdq_linear(x, weights, name, group_size=g), f'w4 ring m={m} g={g} sym={sym}')
+
+
 @pytest.mark.parametrize('n,k', [(1000, 128), (1000, 384), (1000, 5248), (1000, 8448), (16400, 640)])
 def test_w4a16_decode_uneven_wave_splits(gpu, n, k):
     """Decode plans with uneven work: one block (one wave), 3 blocks over 3
