@@ -25,13 +25,16 @@ Also in the same JSON line:
   here with HIP events around a graph of that kernel's launches on the stream
   they run on; ``traffic`` from the committed rocprofv3 counter summary;
 * ``decode_step_kernels``: the same timing for every kernel of the step;
-* ``prefill``: the M=4096 W4A16 GEMM (configs[2]) per shape, TFLOP/s;
+* ``prefill``: the M=4096 W4A16 GEMM per shape, TFLOP/s, next
+  to the vendor library's dense fp16 GEMM (torch.matmul -> hipBLASLt, no
+  dequantization) on the same shape for context;
 * ``batch_sweep``: fused QKV, fused gate_up and a W4 lm_head at
   M in {1, 8, 32, 128, 512}, GB/s and TFLOP/s per launch;
 * ``int8``: configs[0]'s INT8 weight shape on the GPU over a pool of 40
   distinct weights (1.05 GB, past the 256 MB Infinity Cache): weight-only
   W8A16 and W8A8 (``int8_gemm``) decode GB/s, M=4096 W8A16 TFLOP/s and W8A8
-  TOPS against the fp16 / int8 MFMA peaks;
+  TOPS against the fp16 / int8 MFMA peaks, and the vendor library's int8
+  GEMM (torch._int_mm) at M=4096 for context;
 * ``int8_e2e``: the INT8 weight-only model (INT8 v1 tensors, the reference's
   first published row) on the same workload, tok/s;
 * ``setup_seconds``: weight generation, the whole-model repack and the
@@ -523,9 +526,20 @@ def main() -> int:
                 linear(xp[k], layers[0][name + '._prepared'], yp)
             sec = time_graph(torch, g, 10)
             tflops = 2 * 4096 * n * k / sec / 1e12
+            # Context, not a target: the vendor library's dense fp16 GEMM
+            # (torch.matmul -> hipBLASLt) on the same shape with an fp16
+            # weight, no dequantization.
+            wt = (torch.randn(k, n, device=device) * 0.02).half()
+            gv = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gv):
+                torch.matmul(xp[k], wt, out=yp)
+            vsec = time_graph(torch, gv, 10)
             prefill.append({'op': name, 'shape': f'{k}->{n}', 'M': 4096, 'us': round(sec * 1e6, 1),
-                            'tflops': round(tflops, 1), 'frac_fp16_mfma': round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)})
-            del g, yp
+                            'tflops': round(tflops, 1), 'frac_fp16_mfma': round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+                            'vendor_fp16_gemm_us': round(vsec * 1e6, 1),
+                            'vendor_fp16_gemm_tflops': round(2 * 4096 * n * k / vsec / 1e12, 1),
+                            'speed_vs_vendor_fp16': round(vsec / sec, 3)})
+            del g, gv, yp, wt
         result['prefill'] = prefill
 
         # fused QKV and gate_up (every layer's weights in one graph,
@@ -613,6 +627,21 @@ def main() -> int:
                              mfma_peak='int8 5.0 POP/s' if w8a8 else 'fp16 2.5 PFLOP/s')
             int8.append(entry)
             del g
+        # Context for the W8A8 prefill: the vendor library's int8 GEMM
+        # (torch._int_mm -> hipBLASLt, int32 out, no scaling) on the same pool.
+        qx4k_t = qx4k.contiguous()
+        acc32 = torch.empty(4096, HIDDEN, device=device, dtype=torch.int32)
+        wts = [q8w.t().contiguous() for q8w, _, _ in pool[:8]]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for wtq in wts:
+                torch._int_mm(qx4k_t, wtq, out=acc32)
+        sec = time_graph(torch, g, 5) / len(wts)
+        tops = 2 * 4096 * HIDDEN * HIDDEN / sec / 1e12
+        int8.append({'op': 'vendor int8 GEMM, M=4096 (torch._int_mm / hipBLASLt, int32 out; context only)',
+                     'shape': f'{HIDDEN}->{HIDDEN}', 'M': 4096, 'us': round(sec * 1e6, 2), 'tops': round(tops, 1),
+                     'frac_mfma_peak': round(tops / INT8_MFMA_PEAK_TOPS, 4), 'mfma_peak': 'int8 5.0 POP/s'})
+        del g, wts, acc32
         result['int8'] = int8
         del pool, x4k, qx4k, y4k
 
