@@ -94,6 +94,53 @@ def test_two_layers_at_14b_geometry_match_oracle(gpu):
                 f'V cache layer {layer}')
 
 
+def test_int8_two_layers_at_14b_geometry_match_oracle(gpu):
+    """The INT8 weight-only model (INT8 v1 tensors, ``linear_backend=None``)
+    at the same geometry: a 512-token prefill through the W8A16 GEMMs, then
+    graph-replayed decode steps whose RMSNorms, residual adds and SiLU*up run
+    inside the W8A16 GEMVs, against the oracle with fp16(q * s) weights (the
+    reference's int8_weight_only_linear)."""
+    from ondeviceinfer_amd.quantized_model import QuantizedQwen3ForCausalLM
+    from ondeviceinfer_amd.runtime.quantized import QuantizedResidentRuntime, qweight_name, scale_name
+    from ondeviceinfer_amd.weight_quantization.synthetic import random_int8_store
+    cfg = _cfg(2)
+    print('[14b-int8-2l] building the model', flush=True)
+    store = random_int8_store(cfg, seed=1, device=gpu)
+    model = QuantizedQwen3ForCausalLM(store, QuantizedResidentRuntime(store, device=gpu), device=gpu,
+                                      linear_backend=None)
+    layers, linears = [], []
+    for layer in store.layers:
+        np_layer = {k: v.cpu().numpy() for k, v in layer.items()}
+        layers.append(np_layer)
+        linears.append({name: qdq.DecodedLinear(None, weight_fp16=qdq.dequantize_linear_weight(
+            np_layer[qweight_name(name)], np_layer[scale_name(name)])) for name in qwen3.LINEAR_NAMES})
+    lm_head = store.lm_head.cpu().numpy()
+    oracle_model = {'layers': layers, 'linears': linears, 'embed_tokens': store.embed_tokens.cpu().numpy(),
+                    'final_norm': store.final_norm.cpu().numpy(), 'lm_head': lm_head,
+                    'lm_head_linear': qdq.DecodedLinear(None, weight_fp16=lm_head)}
+    prompt = np.random.default_rng(6).integers(0, cfg.vocab_size, 512)
+    cache = model.make_resident_cache(batch_size=1, max_seq_len=600)
+    assert cache._decode_graph is not None and cache._decode_graph.fused
+    ocache = qwen3.KVCacheOracle(cfg.num_hidden_layers)
+    print('[14b-int8-2l] prefill 512 tokens', flush=True)
+    out = model(torch.from_numpy(prompt)[None].to(gpu), cache=cache, logits_to_keep=1)
+    _parity(out.logits[0].float().cpu().numpy(), qwen3.forward(prompt, oracle_model, cfg, ocache, logits_to_keep=1),
+            'int8 prefill 512')
+    token = out.logits[:, -1].argmax(-1, keepdim=True)
+    calls = model.compute_stats.linear_calls
+    for step in range(4):
+        print(f'[14b-int8-2l] decode step {step}', flush=True)
+        out = model(token, cache=cache, logits_to_keep=1)
+        assert out.next_token is not None
+        ref = qwen3.forward(token.cpu().numpy().reshape(-1), oracle_model, cfg, ocache, logits_to_keep=1)
+        _parity(out.logits[0].float().cpu().numpy(), ref, f'int8 decode {step}')
+        token = out.next_token
+    assert model.compute_stats.linear_calls - calls == 4 * 7 * cfg.num_hidden_layers
+    for layer in range(cfg.num_hidden_layers):
+        _parity(cache.key_cache[layer][0, :, :516].float().cpu().numpy(), ocache.k[layer],
+                f'int8 K cache layer {layer}')
+
+
 def test_forty_layers_4096_prompt_graph_against_eager(gpu):
     """Graph decode against the eager path at 40 layers.  Two fp16
     implementations of a 40-layer network drift apart by rounding alone, so
