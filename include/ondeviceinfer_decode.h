@@ -98,6 +98,18 @@ int wq_lm_head_workspace_size(int64_t k, int64_t vocab, size_t* bytes);
 int wq_lm_head(const uint16_t* x, int64_t k, const uint16_t* weight, int64_t vocab, uint16_t* logits,
                int64_t* token, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes for wq_argmax_f16 (per-wave candidates; no initialization
+ * needed). */
+int wq_argmax_f16_workspace_size(int64_t n, size_t* bytes);
+
+/* *token = the first index of the largest of n fp16 values (NaN counts as the
+ * largest), i.e. torch.argmax over a 1-D fp16 tensor; 1 <= n <= 2^30, x
+ * 16-byte aligned.  For logits that another kernel produced (the W4 LM head
+ * of a decode step).  Replaces `output.logits[:, -1].argmax(dim=-1,
+ * keepdim=True)` (generation.py:47, :58) for one token. */
+int wq_argmax_f16(const uint16_t* x, int64_t n, int64_t* token, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,8 @@ _SIGNATURES = {
                             ctypes.c_float, _P, _P, ctypes.c_size_t, _P],
     'wq_prefill_qk_rope': [_P, _I64, _I64, _I64, _I64, _P, _P, ctypes.c_float, _P, _P, _I64, _P, _P, _I64, _P, _P],
     'wq_lm_head_workspace_size': [_I64, _I64, _SIZE_P],
+    'wq_argmax_f16_workspace_size': [_I64, _SIZE_P],
+    'wq_argmax_f16': [_P, _I64, _P, _P, ctypes.c_size_t, _P],
     'wq_lm_head': [_P, _I64, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
 }
 EXPORTED_SYMBOLS = ('wq_last_error', *_SIGNATURES)
@@ -642,3 +644,29 @@ def lm_head(x: torch.Tensor, weight: torch.Tensor, *, logits: torch.Tensor | Non
     _call('wq_lm_head', _ptr(_aligned(x)), k, _ptr(weight), vocab, _ptr(logits), _ptr(token), ws_ptr, ws_bytes,
           _stream(device))
     return logits, token
+
+
+def argmax_f16_workspace_size(n: int) -> int:
+    b = ctypes.c_size_t()
+    _call('wq_argmax_f16_workspace_size', n, ctypes.byref(b))
+    return b.value
+
+
+def argmax_f16(x: torch.Tensor, *, out: torch.Tensor | None = None,
+               workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``torch.argmax`` of a 1-D contiguous fp16 tensor (first index of the
+    largest value, NaN the largest) as one int64 on the device:
+    ``wq_argmax_f16``."""
+    device = _require_gpu(x, out, workspace)
+    if x.dtype != torch.float16 or not x.is_contiguous() or x.numel() < 1:
+        raise ValueError('x must be a non-empty contiguous float16 tensor')
+    n = x.numel()
+    if out is None:
+        out = torch.empty(1, dtype=torch.int64, device=device)
+    elif out.dtype != torch.int64 or out.numel() != 1 or not out.is_contiguous():
+        raise ValueError('out must be one contiguous int64')
+    if workspace is None:
+        workspace = shared_workspace(device, argmax_f16_workspace_size(n), ('argmax_f16', n))
+    _call('wq_argmax_f16', _ptr(_aligned(x)), n, _ptr(out), workspace.data_ptr(),
+          workspace.numel() * workspace.element_size(), _stream(device))
+    return out

@@ -135,6 +135,56 @@ __global__ __launch_bounds__(256) void lm_head_pick_kernel(const float2_t* __res
   if (t == 0) *token = si[0];
 }
 
+// argmax of n fp16 values with the same rules (for logits that a separate
+// kernel produced, e.g. a quantized LM head): each wave keeps the best of a
+// grid-stride walk over 8-value chunks, reduces it over its lanes and leaves
+// one candidate; lm_head_pick_kernel then picks the token.
+constexpr int kArgmaxMaxGroups = 512;   // at most 2048 candidates for the pick
+
+int argmax_grid(int64_t n) {
+  const int64_t g = (n + 256 * 8 - 1) / (256 * 8);
+  return (int)(g < kArgmaxMaxGroups ? g : kArgmaxMaxGroups);
+}
+
+__global__ __launch_bounds__(256) void argmax_f16_kernel(const half_t* __restrict__ x, int64_t n,
+                                                         float2_t* __restrict__ cand) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float best = -INFINITY;
+  int bidx = INT_MAX;
+  const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+  for (int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i0 < n; i0 += stride) {
+    if (i0 + 8 <= n) {
+      const half8_t v = ld_h8(x + i0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = (float)v[e];
+        if (lm_better(f, (int)i0 + e, best, bidx)) {
+          best = f;
+          bidx = (int)i0 + e;
+        }
+      }
+    } else {
+      for (int64_t i = i0; i < n; ++i) {
+        const float f = (float)x[i];
+        if (lm_better(f, (int)i, best, bidx)) {
+          best = f;
+          bidx = (int)i;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o);
+    const int oi = __shfl_xor(bidx, o);
+    if (lm_better(ov, oi, best, bidx)) {
+      best = ov;
+      bidx = oi;
+    }
+  }
+  if (lane == 0) cand[blockIdx.x * 4 + wave] = float2_t{best, __builtin_bit_cast(float, bidx)};
+}
+
 // Enough workgroups to fill the machine once (fewer for a small vocab), and
 // never more than 64 rows per wave.
 int lm_head_grid(int64_t vocab) {
@@ -212,4 +262,32 @@ extern "C" int wq_lm_head(const uint16_t* x, int64_t k, const uint16_t* weight, 
   if (rc1 != WQ_OK || !token) return rc1;
   hipLaunchKernelGGL(lm_head_pick_kernel, dim3(1), dim3(256), 0, s, cand, grid * 4, token);
   return check_launch("lm_head_pick");
+}
+
+extern "C" int wq_argmax_f16_workspace_size(int64_t n, size_t* bytes) {
+  WQ_REQUIRE(bytes, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(n > 0 && n <= INT_MAX / 2, WQ_ERR_INVALID_ARGUMENT, "argmax needs 1 <= n <= 2^30 (got %lld)",
+             (long long)n);
+  *bytes = (size_t)argmax_grid(n) * 4 * sizeof(float2_t);
+  return WQ_OK;
+}
+
+extern "C" int wq_argmax_f16(const uint16_t* x, int64_t n, int64_t* token, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  WQ_REQUIRE(n > 0 && n <= INT_MAX / 2, WQ_ERR_INVALID_ARGUMENT, "argmax needs 1 <= n <= 2^30 (got %lld)",
+             (long long)n);
+  WQ_REQUIRE(x && token, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE((uintptr_t)x % 16 == 0, WQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+  const int grid = argmax_grid(n);
+  const size_t need = (size_t)grid * 4 * sizeof(float2_t);
+  WQ_REQUIRE(workspace && workspace_bytes >= need && (uintptr_t)workspace % 8 == 0, WQ_ERR_WORKSPACE,
+             "argmax needs an 8-byte aligned workspace of %zu bytes (got %zu)", need, workspace_bytes);
+  const hipStream_t s = as_stream(stream);
+  float2_t* cand = reinterpret_cast<float2_t*>(workspace);
+  hipLaunchKernelGGL(argmax_f16_kernel, dim3((unsigned)grid), dim3(256), 0, s, reinterpret_cast<const half_t*>(x), n,
+                     cand);
+  const int rc = check_launch("argmax_f16");
+  if (rc != WQ_OK) return rc;
+  hipLaunchKernelGGL(lm_head_pick_kernel, dim3(1), dim3(256), 0, s, cand, grid * 4, token);
+  return check_launch("argmax_pick");
 }

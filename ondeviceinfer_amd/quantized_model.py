@@ -245,6 +245,9 @@ class DecodeStepGraph:
         self.act = torch.empty(1, cfg.intermediate_size, **f16)
         self.logits = torch.empty(1, cfg.vocab_size, **f16)
         self.next_token = torch.zeros(1, dtype=torch.long, device=dev)
+        self.lm_w4 = model.lm_head_w4
+        self.argmax_ws = torch.zeros(_native.argmax_f16_workspace_size(cfg.vocab_size), dtype=torch.uint8,
+                                     device=dev) if self.lm_w4 is not None else None
         self.native_lm_head = hidden % 512 == 0 and hidden <= 8192 and model.lm_head.is_contiguous()
         self.lm_ws = torch.zeros(max(_native.lm_head_workspace_size(hidden, cfg.vocab_size), 1), dtype=torch.uint8,
                                  device=dev) if self.native_lm_head else None
@@ -329,7 +332,12 @@ class DecodeStepGraph:
         self._lm_head()
 
     def _lm_head(self) -> None:
-        if self.native_lm_head:
+        if self.lm_w4 is not None:
+            p = self.lm_w4
+            _native.w4a16_linear(self.states, p.tiles, p.meta, p.n, p.group_size, out=self.logits,
+                                 workspace=p.workspace)
+            _native.argmax_f16(self.logits.view(-1), out=self.next_token, workspace=self.argmax_ws)
+        elif self.native_lm_head:
             _native.lm_head(self.states.view(-1), self.model.lm_head, logits=self.logits.view(-1),
                             token=self.next_token, workspace=self.lm_ws)
         else:
@@ -382,7 +390,8 @@ class QuantizedQwen3ForCausalLM:
     """
 
     def __init__(self, store, runtime, *, device: str | torch.device, profile_compute: bool = False,
-                 linear_backend: object | None = None, decode_graph: bool = True) -> None:
+                 linear_backend: object | None = None, decode_graph: bool = True,
+                 quantize_lm_head: bool = False) -> None:
         self.store = store
         self.runtime = runtime
         self.config = store.config
@@ -411,10 +420,26 @@ class QuantizedQwen3ForCausalLM:
             if hasattr(linear_backend, 'fuse_projections'):
                 for idx in range(self.config.num_hidden_layers):
                     linear_backend.fuse_projections(runtime.weights_for(idx))
+        # Optional W4 LM head (not in the reference, whose AWQ recipe keeps
+        # lm_head fp16): the fp16 head quantized to uint4 with group-128
+        # scales and zero points, as the decoder linears, and repacked.
+        self.lm_head_w4 = self._quantize_lm_head() if quantize_lm_head else None
         self.decode_graph_enabled = decode_graph and hasattr(self.graph_ops, 'fuse_projections') and \
             self.device.type == 'cuda'
         self._embed_device = None
         self._kv_pool: dict = {}
+
+    def _quantize_lm_head(self, group_size: int = 128):
+        from .weight_quantization.backend import PreparedW4
+        from .weight_quantization.synthetic import awq_quantize
+        vocab, hidden = self.lm_head.shape
+        q = awq_quantize(self.lm_head, group_size)
+        tiles, meta = _native.w4_repack(q['weight_packed'], q['weight_scale'], q['weight_zero_point'], vocab, hidden,
+                                        group_size)
+        del q
+        ws_bytes = _native.w4a16_workspace_size(1, vocab, hidden, group_size)
+        workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=self.device) if ws_bytes else None
+        return PreparedW4(tiles, meta, workspace, hidden, vocab, group_size)
 
     def device_embedding(self) -> Tensor:
         if self._embed_device is None:
@@ -482,5 +507,12 @@ class QuantizedQwen3ForCausalLM:
         if logits_to_keep > 0:
             hidden_states = hidden_states[:, -logits_to_keep:, :].contiguous()
         hidden_states = rms_norm(hidden_states, self.final_norm, self.config.rms_norm_eps)
-        logits = F.linear(hidden_states, self.lm_head)
+        if self.lm_head_w4 is not None:
+            p = self.lm_head_w4
+            flat = hidden_states.reshape(-1, p.k).contiguous()
+            logits = _native.w4a16_linear(flat, p.tiles, p.meta, p.n, p.group_size,
+                                          workspace=p.workspace if flat.shape[0] <= 4 else None)
+            logits = logits.view(*hidden_states.shape[:-1], p.n)
+        else:
+            logits = F.linear(hidden_states, self.lm_head)
         return CausalLMOutput(logits=logits, cache=cache)

@@ -407,3 +407,28 @@ def test_lm_head_only_logits_or_only_token(nat):
                     torch.zeros(8, 640, dtype=torch.float16, device='cuda'))
     with pytest.raises(ValueError, match='workspace'):
         nat.lm_head(tx, tw, workspace=torch.zeros(8, dtype=torch.uint8, device='cuda'))
+
+
+@pytest.mark.parametrize('n', [1, 7, 8, 9, 1000, 2048, 4097, 151936, (1 << 20) + 3])
+def test_argmax_f16_matches_torch(nat, n):
+    """wq_argmax_f16 against torch.argmax on the CPU: random values, a planted
+    tie for the maximum (first index wins), a NaN (wins, first NaN), and all
+    -inf."""
+    print(f'[argmax] n={n}', flush=True)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, generator=g).half()
+    cases = [x.clone()]
+    if n > 3:
+        t = x.clone()
+        t[n // 3] = t[n - 1] = 60000.0
+        cases.append(t)
+        t = x.clone()
+        t[n // 2] = float('nan')
+        t[n - 1] = float('nan')
+        t[0] = float('inf')
+        cases.append(t)
+    cases.append(torch.full((n,), float('-inf')).half())
+    for c in cases:
+        got = nat.argmax_f16(c.cuda())
+        torch.cuda.synchronize()
+        assert got.item() == int(torch.argmax(c.float()).item()), (n, got.item())

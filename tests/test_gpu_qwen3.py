@@ -49,7 +49,7 @@ def numpy_model(cfg, seed=0):
             'lm_head': (rng.standard_normal((cfg.vocab_size, cfg.hidden_size)) * 0.05).astype(np.float16)}
 
 
-def build(np_model, cfg, decode_graph=True):
+def build(np_model, cfg, decode_graph=True, quantize_lm_head=False):
     from ondeviceinfer_amd.config import Qwen3Config
     from ondeviceinfer_amd.quantized_model import QuantizedQwen3ForCausalLM
     from ondeviceinfer_amd.weight_quantization.backend import (CompressedLinearBackend, CompressedResidentRuntime,
@@ -70,7 +70,7 @@ def build(np_model, cfg, decode_graph=True):
     backend = CompressedLinearBackend('marlin')
     runtime = CompressedResidentRuntime(store, backend, device='cuda:0', verbose=False)
     return QuantizedQwen3ForCausalLM(store, runtime, device='cuda:0', linear_backend=backend,
-                                     decode_graph=decode_graph), backend
+                                     decode_graph=decode_graph, quantize_lm_head=quantize_lm_head), backend
 
 
 @pytest.fixture(scope='module')
@@ -153,3 +153,35 @@ def test_greedy_generate_runs_the_reference_loop(tiny):
     top2 = np.sort(logits, axis=-1)[:, -2:]
     decisive = (top2[:, 1] - top2[:, 0]) > 2e-2 * np.abs(logits).max()
     assert np.array_equal(np.argmax(logits, -1)[decisive], gen[decisive])
+
+
+def test_w4_lm_head_prefill_and_graph_decode_match_oracle(tiny):
+    """quantize_lm_head=True: the fp16 LM head quantized to uint4 G=128 and
+    repacked at load; prefill logits through the W4 GEMV/GEMM, decode through
+    the graph's W4 GEMV + wq_argmax_f16, against the oracle decoding the same
+    codes (read back from the tiles with wq_w4_unpack)."""
+    from ondeviceinfer_amd import _native
+    np_model, _, _ = tiny
+    model, _ = build(np_model, TinyCfg, quantize_lm_head=True)
+    p = model.lm_head_w4
+    packed, scale, zero = _native.w4_unpack(p.tiles, p.meta, p.n, p.k, p.group_size)
+    head = {'lm_head.weight_packed': packed.cpu().numpy(), 'lm_head.weight_scale': scale.cpu().numpy(),
+            'lm_head.weight_zero_point': zero.cpu().numpy(),
+            'lm_head.weight_shape': np.array([p.n, p.k], dtype=np.int64)}
+    decoded = qdq.decode_weight(head, 'lm_head.weight')
+    # the quantized head is close to the fp16 one it came from (RTN, 4 bits)
+    assert np.abs(decoded.astype(np.float32) - np_model['lm_head'].astype(np.float32)).max() < 0.05
+    oracle_model = dict(np_model, lm_head_linear=qdq.DecodedLinear(head, 'lm_head.weight'))
+    cache = model.make_resident_cache(batch_size=1, max_seq_len=160)
+    assert cache._decode_graph is not None
+    prompt = np.random.default_rng(3).integers(0, TinyCfg.vocab_size, 70)
+    ocache = qwen3.KVCacheOracle(TinyCfg.num_hidden_layers)
+    out = model(torch.from_numpy(prompt)[None].cuda(), cache=cache, logits_to_keep=5)
+    _ok(out.logits[0], qwen3.forward(prompt, oracle_model, TinyCfg, ocache, logits_to_keep=5), 'w4 head prefill')
+    token = out.logits[:, -1].argmax(-1, keepdim=True)
+    for step in range(4):
+        out = model(token, cache=cache, logits_to_keep=1)
+        ref = qwen3.forward(token.cpu().numpy().reshape(-1), oracle_model, TinyCfg, ocache, logits_to_keep=1)
+        _ok(out.logits[0], ref, f'w4 head decode {step}')
+        assert torch.equal(out.next_token, out.logits[:, -1].argmax(-1, keepdim=True))
+        token = out.next_token
