@@ -37,6 +37,8 @@ Also in the same JSON line:
   GEMM (torch._int_mm) at M=4096 for context;
 * ``int8_e2e``: the INT8 weight-only model (INT8 v1 tensors, the reference's
   first published row) on the same workload, tok/s;
+* ``e2e_w4_lm_head``: the headline workload with the optional W4 LM head
+  (not the reference's configuration), tok/s;
 * ``setup_seconds``: weight generation, the whole-model repack and the
   startup repack of each of layer 0's linears;
 * ``copy_ceiling``: a device-to-device copy's GB/s on the same box;
@@ -660,6 +662,23 @@ def main() -> int:
         result['copy_ceiling'] = {'gbs': round(2 * src.numel() * 2 / sec / 1e9, 1), 'bytes_moved': 2 * src.numel() * 2,
                                   'how': 'torch copy_ of 2 GiB, read+write bytes / time'}
         del src, dst
+
+    if not args.no_extras:
+        # The same model with the optional W4 LM head: 0.39 GB of tiles and
+        # records per token instead of 1.56 GB of fp16.  Not the reference's
+        # configuration (its AWQ recipe keeps lm_head fp16), so not the
+        # headline.
+        log('W4 LM head variant: quantize the head, capture, decode')
+        model.quantize_lm_head()
+        generate(2, 0)
+        _, dec_w4, cache = generate(args.warmup, args.steps)
+        del cache
+        tb, mb = native.w4_repack_size(cfg.vocab_size, cfg.hidden_size, GROUP)
+        result['e2e_w4_lm_head'] = {
+            'workload': 'the headline workload with the LM head quantized to uint4 G=128 (optional; the reference '
+                        'keeps it fp16)', 'tok_s': round(args.steps / dec_w4, 3),
+            'ms_per_token': round(dec_w4 * 1000 / args.steps, 4), 'lm_head_bytes': tb + mb}
+        torch.cuda.empty_cache()
 
     if not args.no_extras:
         log('INT8 weight-only model: build, prefill and decode')

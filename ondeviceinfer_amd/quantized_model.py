@@ -215,8 +215,9 @@ class DecodeStepGraph:
     linear (RMSNorm in its prologue), attention (q/k norm, RoPE, KV append,
     GQA softmax, chunk merge), o linear (+ residual), fused gate_up linear
     (RMSNorm prologue), down linear (SiLU*up prologue, + residual)] -> final
-    norm -> fp16 LM head with the greedy token picked in the same pass, for
-    W4 and INT8 (W8A16) weights alike; other formats (W8A8) take the same
+    norm -> fp16 LM head with the greedy token picked in the same pass (or,
+    with the optional W4 LM head, its GEMV and an argmax), for W4 and INT8
+    (W8A16) weights alike; other formats (W8A8) take the same
     steps with the norms, residual adds and SiLU*up as separate kernels.
     Inputs are the token id and the position (device
     scalars); every launch is a HIP kernel of this library except the
@@ -420,16 +421,21 @@ class QuantizedQwen3ForCausalLM:
             if hasattr(linear_backend, 'fuse_projections'):
                 for idx in range(self.config.num_hidden_layers):
                     linear_backend.fuse_projections(runtime.weights_for(idx))
-        # Optional W4 LM head (not in the reference, whose AWQ recipe keeps
-        # lm_head fp16): the fp16 head quantized to uint4 with group-128
-        # scales and zero points, as the decoder linears, and repacked.
-        self.lm_head_w4 = self._quantize_lm_head() if quantize_lm_head else None
         self.decode_graph_enabled = decode_graph and hasattr(self.graph_ops, 'fuse_projections') and \
             self.device.type == 'cuda'
         self._embed_device = None
         self._kv_pool: dict = {}
+        self.lm_head_w4 = None
+        if quantize_lm_head:
+            self.quantize_lm_head()
 
-    def _quantize_lm_head(self, group_size: int = 128):
+    def quantize_lm_head(self, group_size: int = 128) -> None:
+        """Optional W4 LM head (not in the reference, whose AWQ recipe keeps
+        lm_head fp16): the fp16 head quantized to uint4 with per-group fp16
+        scales and zero points (asymmetric min-max RTN, as the decoder
+        linears) and repacked; the logits of every later call come from the
+        W4 kernels.  Caches made earlier keep the decode graph they captured;
+        new caches capture one with the W4 head."""
         from .weight_quantization.backend import PreparedW4
         from .weight_quantization.synthetic import awq_quantize
         vocab, hidden = self.lm_head.shape
@@ -439,7 +445,8 @@ class QuantizedQwen3ForCausalLM:
         del q
         ws_bytes = _native.w4a16_workspace_size(1, vocab, hidden, group_size)
         workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=self.device) if ws_bytes else None
-        return PreparedW4(tiles, meta, workspace, hidden, vocab, group_size)
+        self.lm_head_w4 = PreparedW4(tiles, meta, workspace, hidden, vocab, group_size)
+        self._kv_pool = {}
 
     def device_embedding(self) -> Tensor:
         if self._embed_device is None:
