@@ -28,6 +28,9 @@ int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const ui
                    hipStream_t s);
 int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
                    half_t* y, hipStream_t s);
+bool w4_gemm_small_fits(int64_t M, int64_t N);
+int launch_w4_gemm_small(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
+                         half_t* y, hipStream_t s);
 
 int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                          int x_mode, const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
@@ -100,6 +103,9 @@ extern "C" int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const vo
              WQ_ERR_INVALID_ARGUMENT, "x, tiles and y must be 16-byte aligned and meta 8-byte aligned");
   const half_t* xh = reinterpret_cast<const half_t*>(x);
   half_t* yh = reinterpret_cast<half_t*>(y);
+  if (w4_gemm_small_fits(m, n) && k <= kGemmMaxK)
+    return launch_w4_gemm_small(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
+                                reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
   if (m <= kSkinnyMaxM)
     return launch_w4_skinny(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
                             reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, workspace,

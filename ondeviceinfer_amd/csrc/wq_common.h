@@ -86,8 +86,10 @@ __device__ __forceinline__ uint4_t lds_read16_asm(const uint8_t* p) {
 // fragments it completes so that no use moves above it.
 template <int MT>
 __device__ __forceinline__ void lds_wait_first_half(uint4_t (&b)[MT]) {
-  static_assert(MT == 2 || MT == 4 || MT == 8 || MT == 16, "fragment count");
-  if constexpr (MT == 16) {
+  static_assert(MT == 1 || MT == 2 || MT == 4 || MT == 8 || MT == 16, "fragment count");
+  if constexpr (MT == 1) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[0]));   // a single read: all of it
+  } else if constexpr (MT == 16) {
     asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]),
                  "+v"(b[6]), "+v"(b[7]));
   } else if constexpr (MT == 8) {
@@ -100,8 +102,10 @@ __device__ __forceinline__ void lds_wait_first_half(uint4_t (&b)[MT]) {
 }
 template <int MT>
 __device__ __forceinline__ void lds_wait_rest(uint4_t (&b)[MT]) {
-  static_assert(MT == 2 || MT == 4 || MT == 8 || MT == 16, "fragment count");
-  if constexpr (MT == 16) {
+  static_assert(MT == 1 || MT == 2 || MT == 4 || MT == 8 || MT == 16, "fragment count");
+  if constexpr (MT == 1) {
+    // completed by lds_wait_first_half
+  } else if constexpr (MT == 16) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[8]), "+v"(b[9]), "+v"(b[10]), "+v"(b[11]), "+v"(b[12]), "+v"(b[13]),
                  "+v"(b[14]), "+v"(b[15]));
   } else if constexpr (MT == 8) {

@@ -170,6 +170,25 @@ def test_w4a16_skinny_load_ring_long_k(gpu, m, g, sym):
     check_parity(host(y), qdq.qdq_linear(x, weights, name, group_size=g), f'w4 ring m={m} g={g} sym={sym}')
 
 
+@pytest.mark.parametrize('n,k,g,sym', [(32776, 640, 128, False),    # 2049 tiles, one per wave; 5 blocks
+                                       (65544, 768, 128, True),     # 4097 tiles, two per wave, the last alone
+                                       (32768, 2048, 256, False),   # groups of 256
+                                       (32768, 128, 128, False)])   # a single block: the ring runs out at once
+def test_w4a16_deep_ring_wide_n(gpu, n, k, g, sym):
+    """The deep-ring GEMM (wide N, 16 < M <= 64): every output against the
+    oracle at M = 17, 31, 32, 33, 50 and 64, and bit-identical to the same
+    rows of an M = 65 call, which runs the prefill GEMM."""
+    name = 'p.weight'
+    weights, x = synth.w4_case(n, k, 65, seed=k + n % 11, group_size=g, symmetric=sym, name=name)
+    backend, layer = prepared_w4(weights, name, gpu, group_size=g)
+    w = qdq.decode_weight(weights, name, group_size=g)
+    y65 = host(backend.linear(dev(x, gpu), layer, name))
+    for m in (17, 31, 32, 33, 50, 64):
+        y = host(backend.linear(dev(x[:m], gpu), layer, name))
+        check_parity(y, qdq.linear_fp32(x[:m], w), f'w4 deep n={n} k={k} g={g} m={m}')
+        assert np.array_equal(bits(y), bits(y65[:m])), f'deep ring vs prefill GEMM m={m}'
+
+
 @pytest.mark.parametrize('n,k', [(1000, 128), (1000, 384), (1000, 5248), (1000, 8448), (16400, 640)])
 def test_w4a16_decode_uneven_wave_splits(gpu, n, k):
     """Decode plans with uneven work: one block (one wave), 3 blocks over 3
