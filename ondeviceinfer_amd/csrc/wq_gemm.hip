@@ -142,11 +142,29 @@ __device__ __forceinline__ void gemm_store(const float4_t (&acc)[NT][MT], int ti
   }
 }
 
+// Workgroup -> (n slice bx, row block by).  Workgroups go to the 8 XCDs
+// round-robin by flat id.  With rpx > 0 (the host sets it when the row blocks
+// divide by 8: rpx = row blocks / 8), XCD x takes row blocks
+// [x*rpx, (x+1)*rpx) with every n slice, row block fastest, so the
+// workgroups resident on one XCD at a time share a few activation row blocks
+// and a few weight slices in that XCD's L2.
+__device__ __forceinline__ void gemm_coords(int rpx, int& bx, int& by) {
+  if (rpx > 0) {
+    const int b = blockIdx.x + gridDim.x * blockIdx.y;
+    const int local = b >> 3;
+    by = (b & 7) * rpx + local % rpx;
+    bx = local / rpx;
+  } else {
+    bx = blockIdx.x;
+    by = blockIdx.y;
+  }
+}
+
 template <GFmt F, int NT, int MT>
 __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restrict__ x, int M, int K,
                                                          const void* __restrict__ wsrc,
                                                          const void* __restrict__ wmeta, int N, int bpg,
-                                                         const half_t* __restrict__ bias, half_t* __restrict__ y) {
+                                                         const half_t* __restrict__ bias, half_t* __restrict__ y, int rpx) {
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kRowBytes;
   constexpr int kInstrPerWave = BM * 16 / 64 / 4;   // 1 KiB direct loads per wave per stage
@@ -157,8 +175,10 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
   const int i = lane & 15, kb = lane >> 4;
   const int ntile = (N + 15) >> 4;
   const int nblk = K / kW4BlockK;
-  const int m0 = blockIdx.y * BM;
-  const int tile0 = ((int)blockIdx.x * 4 + wave) * NT;
+  int bx, by;
+  gemm_coords(rpx, bx, by);
+  const int m0 = by * BM;
+  const int tile0 = (bx * 4 + wave) * NT;
 
   // Activation copy for block `blk` into stage `st`: instruction J of the
   // workgroup fills rows 4J..4J+3; lane L lands in row 4J + L/16, slot L%16,
@@ -281,8 +301,10 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
   const int i = lane & 15, kb = lane >> 4;
   const int ntile = (N + 15) >> 4;
   const int nblk = K / kW4BlockK;
-  const int m0 = blockIdx.y * BM;
-  const int tile0 = ((int)blockIdx.x * 4 + wave) * NT;
+  int bx, by;
+  gemm_coords(0, bx, by);
+  const int m0 = by * BM;
+  const int tile0 = (bx * 4 + wave) * NT;
 
   // Activation copy as in wq_gemm_kernel: instruction J of the workgroup
   // fills rows 4J..4J+3 with lane L in row 4J + L/16, slot L%16.
@@ -383,7 +405,11 @@ int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, 
                 const half_t* bias, half_t* y, hipStream_t s) {
   const int ntile = (N + 15) / 16;
   const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)));
-  hipLaunchKernelGGL((wq_gemm_kernel<F, NT, MT>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y);
+  // Row blocks owned per XCD from M = 4096 on, for W4 (M = 4096: fused gate_up
+  // 1274 -> 1241 us, down 681 -> 665 us; at M = 2048 it slows the down
+  // projection, and the W8 GEMM gains nothing).
+  const int rpx = F == GFmt::W4 && M >= 4096 && grid.y % 8 == 0 ? (int)grid.y / 8 : 0;
+  hipLaunchKernelGGL((wq_gemm_kernel<F, NT, MT>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y, rpx);
   return check_launch(F == GFmt::W4 ? "w4_gemm" : "w8_gemm");
 }
 
@@ -396,19 +422,28 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
   return check_launch(F == GFmt::W4 ? "w4_gemm_deep" : "w8_gemm_deep");
 }
 
-// 256-wide n slices when the grid still covers the machine twice over, else
-// 64-wide slices.  The narrow form takes 64-row x tiles up to M = 256
-// (32 KiB of LDS, five workgroups per CU): with 128 rows its grids sit just
-// above one round of the 512 resident workgroups (M = 128: fused QKV 40.9 ->
-// 33.3 us, gate_up 94 -> 86 us; the wide form keeps 128 rows, whose weights
-// are then streamed half as often).
+// Grids: 256-wide n slices of 128-row tiles (NT = 4, MT = 8) when that still
+// covers the machine twice over.  Otherwise, for W4, 128-wide slices of
+// 64-row tiles (NT = 2, MT = 4) above M = 256 and for the wide small-M grids,
+// else 64-wide slices (NT = 1): a narrow shape's activations are then read
+// half as often (M = 2048: 5120^2 155 -> 127 us, 17408->5120 498 -> 423 us;
+// M = 4096: 5120->1024 63 -> 57 us), a wide one keeps more weight tiles per
+// activation fragment (M = 128 fused gate_up 85.5 -> 72.7 us).  The W8
+// weight loads (16 rows x 64 B) lose from two tiles per wave: W8 keeps 64-wide
+// slices of 64-row (M <= 256) or 128-row tiles.
 template <GFmt F>
 int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
                      const half_t* bias, half_t* y, hipStream_t s) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128;
   if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
-  if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
-  return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
+  if constexpr (F == GFmt::W4) {
+    if (M > 256 || ((ntile + 7) / 8) * ((M + 63) / 64) >= 384)
+      return launch_gemm<F, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
+    return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
+  } else {
+    if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
+    return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
+  }
 }
 
 }  // namespace
