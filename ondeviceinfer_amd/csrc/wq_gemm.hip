@@ -288,7 +288,8 @@ template <GFmt F, int NT, int MT, int D>
 __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restrict__ x, int M, int K,
                                                            const void* __restrict__ wsrc,
                                                            const void* __restrict__ wmeta, int N, int bpg,
-                                                           const half_t* __restrict__ bias, half_t* __restrict__ y) {
+                                                           const half_t* __restrict__ bias, half_t* __restrict__ y,
+                                                           int rpx) {
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kRowBytes;
   constexpr int kInstrPerWave = BM * 16 / 64 / 4;   // 1 KiB direct loads per wave per stage
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
   const int ntile = (N + 15) >> 4;
   const int nblk = K / kW4BlockK;
   int bx, by;
-  gemm_coords(0, bx, by);
+  gemm_coords(rpx, bx, by);
   const int m0 = by * BM;
   const int tile0 = (bx * 4 + wave) * NT;
 
@@ -400,16 +401,21 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
   gemm_store<F, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, wmeta, bias, y);
 }
 
+// Row blocks owned per XCD (gemm_coords) from M = 4096 on, for W4 (M = 4096:
+// fused gate_up 1274 -> 1241 us, down 681 -> 665 us; at M = 2048 it slows the
+// down projection, and the W8 GEMM gains nothing); 0 = launch order.
+template <GFmt F>
+int xcd_rows(int M, unsigned grid_y) {
+  return F == GFmt::W4 && M >= 4096 && grid_y % 8 == 0 ? (int)grid_y / 8 : 0;
+}
+
 template <GFmt F, int NT, int MT>
 int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
                 const half_t* bias, half_t* y, hipStream_t s) {
   const int ntile = (N + 15) / 16;
   const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)));
-  // Row blocks owned per XCD from M = 4096 on, for W4 (M = 4096: fused gate_up
-  // 1274 -> 1241 us, down 681 -> 665 us; at M = 2048 it slows the down
-  // projection, and the W8 GEMM gains nothing).
-  const int rpx = F == GFmt::W4 && M >= 4096 && grid.y % 8 == 0 ? (int)grid.y / 8 : 0;
-  hipLaunchKernelGGL((wq_gemm_kernel<F, NT, MT>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y, rpx);
+  hipLaunchKernelGGL((wq_gemm_kernel<F, NT, MT>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y,
+                     xcd_rows<F>(M, grid.y));
   return check_launch(F == GFmt::W4 ? "w4_gemm" : "w8_gemm");
 }
 
@@ -418,28 +424,32 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
                      const half_t* bias, half_t* y, hipStream_t s) {
   const int ntile = (N + 15) / 16;
   const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)));
-  hipLaunchKernelGGL((wq_gemm_deep_kernel<F, NT, MT, D>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y);
+  hipLaunchKernelGGL((wq_gemm_deep_kernel<F, NT, MT, D>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y,
+                     xcd_rows<F>(M, grid.y));
   return check_launch(F == GFmt::W4 ? "w4_gemm_deep" : "w8_gemm_deep");
 }
 
 // Grids: 256-wide n slices of 128-row tiles (NT = 4, MT = 8) when that still
-// covers the machine twice over.  Otherwise, for W4, 128-wide slices of
-// 64-row tiles (NT = 2, MT = 4) above M = 256 and for the wide small-M grids,
-// else 64-wide slices (NT = 1): a narrow shape's activations are then read
-// half as often (M = 2048: 5120^2 155 -> 127 us, 17408->5120 498 -> 423 us;
-// M = 4096: 5120->1024 63 -> 57 us), a wide one keeps more weight tiles per
-// activation fragment (M = 128 fused gate_up 85.5 -> 72.7 us).  The W8
-// weight loads (16 rows x 64 B) lose from two tiles per wave: W8 keeps 64-wide
-// slices of 64-row (M <= 256) or 128-row tiles.
+// covers the machine twice over.  Otherwise W4 takes the most work per
+// workgroup that still gives at least 384 workgroups: 128-wide slices of
+// 64-row tiles (NT = 2, MT = 4), then 64-wide slices (NT = 1), then 64-wide
+// slices of 32-row tiles on the deep ring (NT = 1, MT = 2, D = 6).  The
+// narrow shapes gain most (k_proj 5120->1024: M = 2048 46.7 -> 38.0 us,
+// M = 512 37.4 -> 21.8 us; down 17408->5120 at M = 128 101 -> 77 us; 5120^2
+// at M = 2048 155 -> 127 us).  The W8 weight loads (16 rows x 64 B) lose from
+// two tiles per wave: W8 keeps 64-wide slices of 64-row (M <= 256) or 128-row
+// tiles.
 template <GFmt F>
 int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
                      const half_t* bias, half_t* y, hipStream_t s) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128;
   if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
   if constexpr (F == GFmt::W4) {
-    if (M > 256 || ((ntile + 7) / 8) * ((M + 63) / 64) >= 384)
-      return launch_gemm<F, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
-    return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
+    constexpr long kMinGrid = 384;
+    const long mb64 = (M + 63) / 64;
+    if (((ntile + 7) / 8) * mb64 >= kMinGrid) return launch_gemm<F, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
+    if (((ntile + 3) / 4) * mb64 >= kMinGrid) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
+    return launch_gemm_deep<F, 1, 2, 6>(x, M, K, w, meta, N, bpg, bias, y, s);
   } else {
     if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
     return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
