@@ -266,10 +266,12 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
   gemm_store<F, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, wmeta, bias, y);
 }
 
-// Small-M form (16 < M <= 64 on wide N): the same tiles and block math, so
-// bit-identical results, with D - 1 blocks of activations (an LDS ring of D
-// stages) and weights (D register sets) in flight instead of one, so a small
-// M's short per-block math does not wait out each block's load latency.  The
+// Deep-ring form, for grids whose per-block math is short (wide N at
+// 16 < M <= 64, and the smallest prefill grids on 32-row tiles): the same
+// tiles and block math, so bit-identical results, with D - 1 blocks of
+// activations (an LDS ring of D stages) and weights (D register sets) in
+// flight instead of one, so the math does not wait out each block's load
+// latency.  The
 // block loop is unrolled by D so every stage and register set is a constant;
 // the loads of blocks past the last (the ring's run-out) are empty and never
 // used.  Per block: wait until block b+1's loads have landed (vmcnt = the
