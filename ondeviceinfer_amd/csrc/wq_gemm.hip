@@ -18,6 +18,10 @@
 // W4 weights are dequantized with their group scale, fp16((q - z) * s): the
 // oracle's fp16 weight bit for bit.  INT8 weights enter as exact fp16 q and
 // the per-row scale multiplies the fp32 sum in the epilogue.
+// The tile shape follows the grid size (launch_gemm_auto); grids whose
+// blocks are too short to hide a load run a deep-ring form with several
+// blocks in flight (wq_gemm_deep_kernel), with the same block math; from
+// M = 4096 on, W4 row blocks are assigned to XCDs (gemm_coords).
 #include "wq_common.h"
 #include "wq_status.h"
 
