@@ -583,13 +583,16 @@ def main() -> int:
         # 5120x5120 weights (N(0, 0.02), per-channel symmetric INT8; 1.05 GB,
         # above the 256 MB Infinity Cache), each case a graph of one launch
         # per weight: weight-only W8A16 decode, W8A8 (int8_gemm) decode and
-        # the M=4096 W8A16 / W8A8 prefill GEMMs on the matrix cores.
+        # the M=4096 W8A16 / W8A8 prefill GEMMs on the matrix cores, over the
+        # INT8 tiles the prepared linears stream (wq_w8_repack), and the
+        # W8A16 pair once more over the row-major weight as stored.
         g0 = torch.Generator(device=device).manual_seed(0)
-        pool = []
+        pool, rowmajor = [], []
         for _ in range(40):
             w8 = (torch.randn(HIDDEN, HIDDEN, device=device, generator=g0) * 0.02).half()
             q8w, s8w = native.w8_quantize(w8)
-            pool.append((q8w, s8w, s8w.float()))
+            pool.append((native.w8_repack(q8w), s8w, s8w.float()))
+            rowmajor.append((q8w, s8w, s8w.float()))
         del w8
         int8 = []
         x1 = torch.randn(1, HIDDEN, device=device).half()
@@ -599,22 +602,27 @@ def main() -> int:
         y1 = torch.empty(1, HIDDEN, device=device, dtype=torch.float16)
         y4k = torch.empty(4096, HIDDEN, device=device, dtype=torch.float16)
         cases = [
-            ('w8a16 decode (configs[0] on the GPU)', 1, 'w8a16',
+            ('w8a16 decode (configs[0] on the GPU)', 1, 'w8a16', pool,
              lambda q, s, s32: native.w8a16_linear(x1, q, s, out=y1)),
-            ('w8a8 int8_gemm decode (quantize + linear)', 1, 'w8a8',
+            ('w8a8 int8_gemm decode (quantize + linear)', 1, 'w8a8', pool,
              lambda q, s, s32: native.w8a8_linear(*native.w8a8_quantize(x1), q, s32, out=y1)),
-            ('w8a8 linear only, decode', 1, 'w8a8', lambda q, s, s32: native.w8a8_linear(qx1, sx1, q, s32, out=y1)),
-            ('w8a16 prefill M=4096', 4096, 'w8a16', lambda q, s, s32: native.w8a16_linear(x4k, q, s, out=y4k)),
-            ('w8a8 linear only, prefill M=4096', 4096, 'w8a8',
+            ('w8a8 linear only, decode', 1, 'w8a8', pool,
+             lambda q, s, s32: native.w8a8_linear(qx1, sx1, q, s32, out=y1)),
+            ('w8a16 prefill M=4096', 4096, 'w8a16', pool, lambda q, s, s32: native.w8a16_linear(x4k, q, s, out=y4k)),
+            ('w8a8 linear only, prefill M=4096', 4096, 'w8a8', pool,
              lambda q, s, s32: native.w8a8_linear(qx4k, sx4k, q, s32, out=y4k)),
+            ('w8a16 decode, row-major weight as stored', 1, 'w8a16', rowmajor,
+             lambda q, s, s32: native.w8a16_linear(x1, q, s, out=y1)),
+            ('w8a16 prefill M=4096, row-major weight as stored', 4096, 'w8a16', rowmajor,
+             lambda q, s, s32: native.w8a16_linear(x4k, q, s, out=y4k)),
         ]
-        for label, mm, kind, fn in cases:
-            fn(*pool[0])
+        for label, mm, kind, weights, fn in cases:
+            fn(*weights[0])
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                for q8w, s8w, s32 in pool:
+                for q8w, s8w, s32 in weights:
                     fn(q8w, s8w, s32)
-            sec = time_graph(torch, g, 5) / len(pool)
+            sec = time_graph(torch, g, 5) / len(weights)
             w8a8 = kind == 'w8a8'   # int8 x and fp32 scales vs fp16 x and fp16 scales
             b = HIDDEN * HIDDEN + (4 if w8a8 else 2) * HIDDEN + (1 if w8a8 else 2) * mm * HIDDEN + 2 * mm * HIDDEN
             entry = {'op': label, 'shape': f'{HIDDEN}->{HIDDEN}', 'M': mm, 'us': round(sec * 1e6, 2),
@@ -633,7 +641,7 @@ def main() -> int:
         # (torch._int_mm -> hipBLASLt, int32 out, no scaling) on the same pool.
         qx4k_t = qx4k.contiguous()
         acc32 = torch.empty(4096, HIDDEN, device=device, dtype=torch.int32)
-        wts = [q8w.t().contiguous() for q8w, _, _ in pool[:8]]
+        wts = [q8w.t().contiguous() for q8w, _, _ in rowmajor[:8]]
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for wtq in wts:
@@ -645,7 +653,7 @@ def main() -> int:
                      'frac_mfma_peak': round(tops / INT8_MFMA_PEAK_TOPS, 4), 'mfma_peak': 'int8 5.0 POP/s'})
         del g, wts, acc32
         result['int8'] = int8
-        del pool, x4k, qx4k, y4k
+        del pool, rowmajor, x4k, qx4k, y4k
 
         # Copy ceiling: 2 GiB device-to-device copy (read + write bytes).
         src = torch.empty(2**30, dtype=torch.uint16, device=device)

@@ -188,6 +188,33 @@ int wq_w8a16_decode_fused(const uint16_t* x, int64_t k, const int8_t* qweight, c
                           float eps, const uint16_t* residual, float* sumsq_out, uint16_t* y, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/* INT8 tile layout (k % 128 == 0): the same int8 values as the row-major
+ * [n, k] weight, regrouped into 2 KiB per (16-row tile, 128-k block), rows
+ * past n zero, so that each 16-byte-per-lane piece the INT8 kernels take is
+ * one contiguous 1 KiB wave load instead of sixteen 64-byte row segments.
+ * Within tile t, block b: byte 1024 p + 16 l + j = q[16t + l % 16]
+ * [128b + 64p + 16 (l / 16) + j], p in {0, 1}, l in [0, 64), j in [0, 16).
+ * Like the W4 tile layout, this one is this library's own (the reference
+ * stores INT8 row-major and dequantizes it, quantized_model.py:101-106);
+ * wq_w8_repack / wq_w8_unpack are a bit-exact pair and the _tiled linears
+ * below return the same bits as their row-major counterparts. */
+int wq_w8_tiles_size(int64_t n, int64_t k, size_t* bytes);
+int wq_w8_repack(const int8_t* qweight, int64_t n, int64_t k, void* tiles, void* stream);
+int wq_w8_unpack(const void* tiles, int64_t n, int64_t k, int8_t* qweight, void* stream);
+
+/* wq_w8a16_linear / wq_w8a16_decode_fused / wq_w8a8_linear over INT8 tiles
+ * (16-byte aligned) instead of the row-major weight; k % 128 == 0.  Same
+ * arguments, results bit-identical.  Replace the same reference calls as
+ * their row-major forms; the decode graph and the prepared INT8 linears of
+ * this library use these. */
+int wq_w8a16_linear_tiled(const uint16_t* x, int64_t m, int64_t k, const void* tiles,
+                          const uint16_t* scale, int64_t n, const uint16_t* bias, uint16_t* y,
+                          void* workspace, size_t workspace_bytes, void* stream);
+int wq_w8a16_decode_fused_tiled(const uint16_t* x, int64_t k, const void* tiles, const uint16_t* scale,
+                                int64_t n, int32_t x_mode, const uint16_t* norm_weight, const float* sumsq_in,
+                                int64_t sumsq_count, float eps, const uint16_t* residual, float* sumsq_out,
+                                uint16_t* y, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Symmetric per-output-channel INT8 quantizer: weight fp32 [n, k] ->
  * qweight int8 [n, k] + fp16 scale [n] (absmax/127, zero rows scale 1,
  * underflowing scales -> smallest fp16 subnormal, the stored scale divides,
@@ -216,6 +243,8 @@ int wq_w8a8_quantize(const uint16_t* x, int64_t m, int64_t k, int8_t* qx, float*
  * (backend.py:254). */
 int wq_w8a8_linear(const int8_t* qx, const float* x_scale, int64_t m, int64_t k, const int8_t* qweight,
                    const float* w_scale, int64_t n, const uint16_t* bias, uint16_t* y, void* stream);
+int wq_w8a8_linear_tiled(const int8_t* qx, const float* x_scale, int64_t m, int64_t k, const void* tiles,
+                         const float* w_scale, int64_t n, const uint16_t* bias, uint16_t* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,7 @@ from __future__ import annotations
 import ctypes
 import threading
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 
@@ -54,7 +55,14 @@ _SIGNATURES = {
                               _P, _P, ctypes.c_size_t, _P],
     'wq_w8a16_decode_fused': [_P, _I64, _P, _P, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P, _P, _P,
                               ctypes.c_size_t, _P],
+    'wq_w8a16_decode_fused_tiled': [_P, _I64, _P, _P, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P, _P, _P,
+                              ctypes.c_size_t, _P],
     'wq_w8_decode': [_P, _P, _I64, _I64, _P, _P],
+    'wq_w8_tiles_size': [_I64, _I64, _SIZE_P],
+    'wq_w8_repack': [_P, _I64, _I64, _P, _P],
+    'wq_w8_unpack': [_P, _I64, _I64, _P, _P],
+    'wq_w8a16_linear_tiled': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
+    'wq_w8a8_linear_tiled': [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P],
     'wq_w8a16_workspace_size': [_I64, _I64, _I64, _SIZE_P],
     'wq_w8a16_linear': [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
     'wq_w8a8_quantize': [_P, _I64, _I64, _P, _P, _P],
@@ -367,17 +375,19 @@ def w4a16_decode_fused(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor,
     return out
 
 
-def w8a16_decode_fused(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, *,
+def w8a16_decode_fused(x: torch.Tensor, qweight, scale: torch.Tensor, *,
                        x_mode: int = X_PLAIN, norm_weight: torch.Tensor | None = None,
                        sumsq_in: torch.Tensor | None = None, eps: float = 1e-6,
                        residual: torch.Tensor | None = None, sumsq_out: torch.Tensor | None = None,
                        out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """The INT8 (row-major [n, k] weight, fp16 row scale) counterpart of
-    ``w4a16_decode_fused`` (``wq_w8a16_decode_fused``)."""
-    device = _require_gpu(x, qweight, scale, norm_weight, sumsq_in, residual, sumsq_out, out, workspace)
-    if qweight.dtype != torch.int8 or qweight.dim() != 2 or not qweight.is_contiguous():
-        raise TypeError('qweight must be a contiguous 2-D INT8 tensor')
-    n, kq = qweight.shape
+    """The INT8 (row-major [n, k] weight or ``W8Tiles``, fp16 row scale)
+    counterpart of ``w4a16_decode_fused`` (``wq_w8a16_decode_fused`` /
+    ``wq_w8a16_decode_fused_tiled``)."""
+    if not isinstance(qweight, W8Tiles) and (qweight.dtype != torch.int8 or qweight.dim() != 2 or
+                                             not qweight.is_contiguous()):
+        raise TypeError('qweight must be a contiguous 2-D INT8 tensor or W8Tiles')
+    n, kq, q, tiled = _w8_weight(qweight)
+    device = _require_gpu(x, q, scale, norm_weight, sumsq_in, residual, sumsq_out, out, workspace)
     if scale.dtype != torch.float16 or scale.numel() != n or not scale.is_contiguous():
         raise ValueError(f'scale must be contiguous float16 with {n} entries')
     k, out = _decode_fused_args(x, n, x_mode, norm_weight, sumsq_in, residual, sumsq_out, out, device)
@@ -386,13 +396,72 @@ def w8a16_decode_fused(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tens
     if workspace is None:
         workspace = shared_workspace(device, w8a16_workspace_size(1, n, k), ('w8a16', 1, n, k))
     ws_ptr, ws_bytes = _ws_args(workspace)
-    _call('wq_w8a16_decode_fused', _ptr(x), k, _ptr(qweight), _ptr(scale), n, x_mode, _ptr(norm_weight),
+    _call('wq_w8a16_decode_fused_tiled' if tiled else 'wq_w8a16_decode_fused', _ptr(x), k, _ptr(q), _ptr(scale), n,
+          x_mode, _ptr(norm_weight),
           _ptr(sumsq_in), 0 if sumsq_in is None else sumsq_in.numel(), float(eps), _ptr(residual), _ptr(sumsq_out),
           _ptr(out), ws_ptr, ws_bytes, _stream(device))
     return out
 
 
 # ----------------------------------------------------------------------------- W8
+
+class W8Tiles(NamedTuple):
+    """An INT8 weight [n, k] in the tile layout the INT8 kernels stream
+    (``wq_w8_repack``): 2 KiB per (16-row tile, 128-k block), each half one
+    contiguous 1 KiB wave load; rows past n are zero.  Same values as the
+    row-major weight, so every linear gives the same bits."""
+    tiles: torch.Tensor   # uint8 [ceil(n/16) * (k/128) * 2048]
+    n: int
+    k: int
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return self.n, self.k
+
+    @property
+    def device(self) -> torch.device:
+        return self.tiles.device
+
+
+def w8_tiles_size(n: int, k: int) -> int:
+    b = ctypes.c_size_t()
+    _call('wq_w8_tiles_size', n, k, ctypes.byref(b))
+    return b.value
+
+
+def w8_repack(qweight: torch.Tensor, out: torch.Tensor | None = None) -> W8Tiles:
+    """Row-major INT8 [n, k] (k % 128 == 0) -> ``W8Tiles``."""
+    device = _require_gpu(qweight, out)
+    if qweight.dtype != torch.int8 or qweight.dim() != 2:
+        raise TypeError(f'expected a 2-D INT8 weight, got {qweight.dtype} {tuple(qweight.shape)}')
+    n, k = qweight.shape
+    size = w8_tiles_size(n, k)
+    if out is None:
+        out = torch.empty(size, dtype=torch.uint8, device=device)
+    else:
+        _check(out, torch.uint8, (size,), 'out')
+    _call('wq_w8_repack', _ptr(_aligned(qweight.contiguous())), n, k, _ptr(out), _stream(device))
+    return W8Tiles(out, n, k)
+
+
+def w8_unpack(w: W8Tiles) -> torch.Tensor:
+    """``W8Tiles`` -> row-major INT8 [n, k] (the inverse of ``w8_repack``)."""
+    device = _require_gpu(w.tiles)
+    _check(w.tiles, torch.uint8, (w8_tiles_size(w.n, w.k),), 'tiles')
+    q = torch.empty((w.n, w.k), dtype=torch.int8, device=device)
+    _call('wq_w8_unpack', _ptr(w.tiles), w.n, w.k, _ptr(q), _stream(device))
+    return q
+
+
+def _w8_weight(qweight) -> tuple[int, int, torch.Tensor, bool]:
+    """(n, k, device buffer, tiled) of a row-major INT8 tensor or ``W8Tiles``."""
+    if isinstance(qweight, W8Tiles):
+        _check(qweight.tiles, torch.uint8, (w8_tiles_size(qweight.n, qweight.k),), 'tiles')
+        return qweight.n, qweight.k, qweight.tiles, True
+    if qweight.dtype != torch.int8 or qweight.dim() != 2:
+        raise TypeError(f'qweight must be a 2-D INT8 tensor or W8Tiles, got {qweight.dtype}')
+    return qweight.shape[0], qweight.shape[1], _aligned(qweight.contiguous()), False
+
 
 def w8_decode(qweight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     device = _require_gpu(qweight, scale)
@@ -407,15 +476,14 @@ def w8_decode(qweight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None,
+def w8a16_linear(x: torch.Tensor, qweight, scale: torch.Tensor, bias: torch.Tensor | None = None,
                  out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """``y = x . (q * scale)^T (+ bias)`` straight from the row-major INT8 weight."""
-    device = _require_gpu(x, qweight, scale, bias, out)
+    """``y = x . (q * scale)^T (+ bias)`` straight from the INT8 weight:
+    row-major [n, k] (``wq_w8a16_linear``) or ``W8Tiles`` (``wq_w8a16_linear_tiled``)."""
+    n, k, q, tiled = _w8_weight(qweight)
+    device = _require_gpu(x, q, scale, bias, out)
     if x.dtype != torch.float16 or x.dim() != 2:
         raise TypeError(f'x must be a 2-D float16 tensor, got {x.dtype} {tuple(x.shape)}')
-    if qweight.dtype != torch.int8 or qweight.dim() != 2:
-        raise TypeError(f'qweight must be a 2-D INT8 tensor, got {qweight.dtype}')
-    n, k = qweight.shape
     if x.shape[1] != k:
         raise ValueError(f'input has {x.shape[1]} features, expected {k}')
     if scale.dtype != torch.float16 or scale.numel() != n:
@@ -424,7 +492,6 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bi
         raise ValueError('bias must be FP16 with one entry per output feature')
     m = x.shape[0]
     x = _aligned(x.contiguous())
-    q = _aligned(qweight.contiguous())
     if out is None:
         out = torch.empty((m, n), dtype=torch.float16, device=device)
     else:
@@ -434,7 +501,7 @@ def w8a16_linear(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, bi
     ws_ptr, ws_bytes = None, 0
     if workspace is not None:
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
-    _call('wq_w8a16_linear', _ptr(x), m, k, _ptr(q), _ptr(scale.contiguous()), n,
+    _call('wq_w8a16_linear_tiled' if tiled else 'wq_w8a16_linear', _ptr(x), m, k, _ptr(q), _ptr(scale.contiguous()), n,
           _ptr(None if bias is None else bias.contiguous()), _ptr(out), ws_ptr, ws_bytes, _stream(device))
     return out
 
@@ -453,29 +520,29 @@ def w8a8_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return qx, scale
 
 
-def w8a8_linear(qx: torch.Tensor, x_scale: torch.Tensor, qweight: torch.Tensor, w_scale: torch.Tensor,
+def w8a8_linear(qx: torch.Tensor, x_scale: torch.Tensor, qweight, w_scale: torch.Tensor,
                 bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """``y = fp16(float(qx . qweight^T) * x_scale[m] * w_scale[n] (+ bias))``,
-    int32 accumulation on the int8 matrix cores (``wq_w8a8_linear``)."""
-    device = _require_gpu(qx, x_scale, qweight, w_scale, bias, out)
-    if qx.dtype != torch.int8 or qx.dim() != 2 or qweight.dtype != torch.int8 or qweight.dim() != 2:
-        raise TypeError('qx and qweight must be 2-D INT8 tensors')
+    int32 accumulation on the int8 matrix cores; ``qweight`` row-major INT8
+    (``wq_w8a8_linear``) or ``W8Tiles`` (``wq_w8a8_linear_tiled``)."""
+    n, kw, q, tiled = _w8_weight(qweight)
+    device = _require_gpu(qx, x_scale, q, w_scale, bias, out)
+    if qx.dtype != torch.int8 or qx.dim() != 2:
+        raise TypeError('qx must be a 2-D INT8 tensor')
     m, k = qx.shape
-    n = qweight.shape[0]
-    if qweight.shape[1] != k:
-        raise ValueError(f'input has {k} features, expected {qweight.shape[1]}')
+    if kw != k:
+        raise ValueError(f'input has {k} features, expected {kw}')
     _check(x_scale, torch.float32, (m,), 'x_scale')
     if w_scale.dtype != torch.float32 or w_scale.numel() != n:
         raise ValueError(f'w_scale must be float32 with {n} entries')
     if bias is not None and (bias.dtype != torch.float16 or bias.numel() != n):
         raise ValueError('bias must be FP16 with one entry per output feature')
     qx = _aligned(qx.contiguous())
-    q = _aligned(qweight.contiguous())
     if out is None:
         out = torch.empty((m, n), dtype=torch.float16, device=device)
     else:
         _check(out, torch.float16, (m, n), 'out')
-    _call('wq_w8a8_linear', _ptr(qx), _ptr(x_scale.contiguous()), m, k, _ptr(q), _ptr(w_scale.contiguous()), n,
+    _call('wq_w8a8_linear_tiled' if tiled else 'wq_w8a8_linear', _ptr(qx), _ptr(x_scale.contiguous()), m, k, _ptr(q), _ptr(w_scale.contiguous()), n,
           _ptr(None if bias is None else bias.contiguous()), _ptr(out), _stream(device))
     return out
 

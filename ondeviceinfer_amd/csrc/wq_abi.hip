@@ -21,13 +21,13 @@ size_t gemv_workspace_bytes(bool w4, int64_t m, int64_t n, int64_t k);
 int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                      half_t* y, void* ws, size_t ws_bytes, hipStream_t s);
 int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
-                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s);
+                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s, int tiled);
 int launch_w8_generic(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
                       half_t* y, hipStream_t s);
 int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
                    hipStream_t s);
 int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
-                   half_t* y, hipStream_t s);
+                   half_t* y, hipStream_t s, int tiled);
 bool w4_gemm_small_fits(int64_t M, int64_t N);
 int launch_w4_gemm_small(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                          half_t* y, hipStream_t s);
@@ -39,7 +39,7 @@ int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uin
 int launch_w8_gemv_fused(const half_t* x, int K, const int8_t* q, const half_t* scale, int N, int x_mode,
                          const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
                          const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
-                         hipStream_t s);
+                         hipStream_t s, int tiled);
 
 // Largest M served by the MFMA GEMV (4 chunks of 16 activation rows).
 constexpr int64_t kSkinnyMaxM = 64;
@@ -148,10 +148,15 @@ extern "C" int wq_w4a16_decode_fused(const uint16_t* x, int64_t k, const void* t
                               workspace, workspace_bytes, as_stream(stream));
 }
 
-extern "C" int wq_w8a16_decode_fused(const uint16_t* x, int64_t k, const int8_t* qweight, const uint16_t* scale,
-                                     int64_t n, int32_t x_mode, const uint16_t* norm_weight, const float* sumsq_in,
-                                     int64_t sumsq_count, float eps, const uint16_t* residual, float* sumsq_out,
-                                     uint16_t* y, void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+// INT8 weight-only entry points over either weight layout (W8Layout): the
+// caller's row-major [N, K] qweight (tiled = 0) or wq_w8_repack's tiles
+// (tiled = 1, which needs k % 128 == 0).
+int w8a16_decode_fused_impl(const uint16_t* x, int64_t k, const int8_t* qweight, const uint16_t* scale, int64_t n,
+                            int32_t x_mode, const uint16_t* norm_weight, const float* sumsq_in, int64_t sumsq_count,
+                            float eps, const uint16_t* residual, float* sumsq_out, uint16_t* y, void* workspace,
+                            size_t workspace_bytes, void* stream, int tiled) {
   if (int st = linear_shape_check(1, n, k)) return st;
   WQ_REQUIRE(n % 16 == 0 && k % kW8BlockK == 0, WQ_ERR_UNSUPPORTED,
              "fused decode linear needs n %% 16 == 0 and k %% 128 == 0 (n=%lld k=%lld)", (long long)n, (long long)k);
@@ -166,26 +171,75 @@ extern "C" int wq_w8a16_decode_fused(const uint16_t* x, int64_t k, const int8_t*
                               reinterpret_cast<const half_t*>(scale), (int)n, x_mode,
                               reinterpret_cast<const half_t*>(norm_weight), sumsq_in, (int)sumsq_count, eps,
                               reinterpret_cast<const half_t*>(residual), sumsq_out, reinterpret_cast<half_t*>(y),
-                              workspace, workspace_bytes, as_stream(stream));
+                              workspace, workspace_bytes, as_stream(stream), tiled);
 }
 
-extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight, const uint16_t* scale,
-                               int64_t n, const uint16_t* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+int w8a16_linear_impl(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight, const uint16_t* scale,
+                      int64_t n, const uint16_t* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
+                      void* stream, int tiled) {
   if (int st = linear_shape_check(m, n, k)) return st;
   WQ_REQUIRE(qweight && scale, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(!tiled || (k % kW8BlockK == 0 && aligned16(qweight)), WQ_ERR_UNSUPPORTED,
+             "INT8 tiles need k %% 128 == 0 and 16-byte aligned tiles (k=%lld)", (long long)k);
   if (m == 0) return WQ_OK;   // empty activations: x and y may be null
   WQ_REQUIRE(x && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
   const half_t* xh = reinterpret_cast<const half_t*>(x);
   const half_t* sh = reinterpret_cast<const half_t*>(scale);
   const half_t* bh = reinterpret_cast<const half_t*>(bias);
   half_t* yh = reinterpret_cast<half_t*>(y);
+  if (tiled) {
+    WQ_REQUIRE(aligned16(x), WQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if (m <= kSkinnyMaxM)
+      return launch_w8_skinny(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, workspace, workspace_bytes,
+                              as_stream(stream), 1);
+    if (k <= kGemmMaxK) return launch_w8_gemm(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream), 1);
+    for (int64_t r = 0; r < m; r += kSkinnyMaxM) {   // k beyond the GEMM's offsets: 64 rows at a time
+      const int64_t mr = m - r < kSkinnyMaxM ? m - r : kSkinnyMaxM;
+      const int rc = launch_w8_skinny(xh + r * k, (int)mr, (int)k, qweight, sh, bh, (int)n, yh + r * n, workspace,
+                                      workspace_bytes, as_stream(stream), 1);
+      if (rc != WQ_OK) return rc;
+    }
+    return WQ_OK;
+  }
   if (k % kW8BlockK != 0 || !aligned16(x) || !aligned16(qweight) || (m > kSkinnyMaxM && k > kGemmMaxK))
     return launch_w8_generic(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
   if (m <= kSkinnyMaxM)
     return launch_w8_skinny(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, workspace, workspace_bytes,
-                            as_stream(stream));
-  return launch_w8_gemm(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream));
+                            as_stream(stream), 0);
+  return launch_w8_gemm(xh, (int)m, (int)k, qweight, sh, bh, (int)n, yh, as_stream(stream), 0);
+}
+
+}  // namespace
+
+extern "C" int wq_w8a16_decode_fused(const uint16_t* x, int64_t k, const int8_t* qweight, const uint16_t* scale,
+                                     int64_t n, int32_t x_mode, const uint16_t* norm_weight, const float* sumsq_in,
+                                     int64_t sumsq_count, float eps, const uint16_t* residual, float* sumsq_out,
+                                     uint16_t* y, void* workspace, size_t workspace_bytes, void* stream) {
+  return w8a16_decode_fused_impl(x, k, qweight, scale, n, x_mode, norm_weight, sumsq_in, sumsq_count, eps, residual,
+                                 sumsq_out, y, workspace, workspace_bytes, stream, 0);
+}
+
+extern "C" int wq_w8a16_decode_fused_tiled(const uint16_t* x, int64_t k, const void* tiles, const uint16_t* scale,
+                                           int64_t n, int32_t x_mode, const uint16_t* norm_weight,
+                                           const float* sumsq_in, int64_t sumsq_count, float eps,
+                                           const uint16_t* residual, float* sumsq_out, uint16_t* y, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  return w8a16_decode_fused_impl(x, k, reinterpret_cast<const int8_t*>(tiles), scale, n, x_mode, norm_weight,
+                                 sumsq_in, sumsq_count, eps, residual, sumsq_out, y, workspace, workspace_bytes,
+                                 stream, 1);
+}
+
+extern "C" int wq_w8a16_linear(const uint16_t* x, int64_t m, int64_t k, const int8_t* qweight, const uint16_t* scale,
+                               int64_t n, const uint16_t* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  return w8a16_linear_impl(x, m, k, qweight, scale, n, bias, y, workspace, workspace_bytes, stream, 0);
+}
+
+extern "C" int wq_w8a16_linear_tiled(const uint16_t* x, int64_t m, int64_t k, const void* tiles,
+                                     const uint16_t* scale, int64_t n, const uint16_t* bias, uint16_t* y,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  return w8a16_linear_impl(x, m, k, reinterpret_cast<const int8_t*>(tiles), scale, n, bias, y, workspace,
+                           workspace_bytes, stream, 1);
 }
 
 // ---------------------------------------------------------------------------

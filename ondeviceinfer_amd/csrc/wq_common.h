@@ -29,6 +29,28 @@ typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 constexpr int kW4BlockK = 128;     // k extent of one W4 tile block (one 1 KiB wave load)
 constexpr int kW4MetaBytes = 40;   // per (16-row tile, group): 16 fp16 scales + 2 zero words
 constexpr int kW8BlockK = 128;     // k extent of one INT8 wave block (2 x 16 B per lane)
+constexpr int kW8TileBlockBytes = 16 * kW8BlockK;   // one (16-row tile, 128-k block) of INT8 tiles
+
+// INT8 weight addressing, shared by the W8A16 and W8A8 kernels.  For 16-row
+// tile t and 128-k block b, lane l = (i, kb) = (l % 16, l / 16) of a wave
+// takes piece 0 = bytes k = 128b + 16kb .. +15 and piece 1 = bytes
+// k = 128b + 64 + 16kb .. +15 of row 16t + i.
+//  * row-major q [N, K]: the lane's base is row * K + 16kb (rows clamped to
+//    N - 1, never stored), a block is 128 bytes on, piece 1 64 bytes on;
+//  * tiles (wq_w8_repack): 2 KiB per (tile, block), piece p at +1024p and
+//    lane l at +16l, so that each piece is one contiguous 1 KiB wave load;
+//    the lane's base is t * nblk * 2048 + 16l, a block 2048 bytes on,
+//    piece 1 1024 bytes on (rows past N are zero in the tiles).
+struct W8Layout {
+  int tiled;
+  __device__ __forceinline__ int block_bytes() const { return tiled ? kW8TileBlockBytes : kW8BlockK; }
+  __device__ __forceinline__ int piece1() const { return tiled ? kW8TileBlockBytes / 2 : 64; }
+  __device__ __forceinline__ size_t lane_base(int tile, int lane, int N, int K) const {
+    if (tiled) return (size_t)tile * (K / kW8BlockK) * kW8TileBlockBytes + 16 * lane;
+    const int row = (tile * 16 + (lane & 15)) < N ? tile * 16 + (lane & 15) : N - 1;
+    return (size_t)row * K + 16 * (lane >> 4);
+  }
+};
 // Word 3 of a gfx9 buffer resource: 32-bit data format, so raw dword loads
 // are range-checked against num_records and return 0 past it.
 constexpr int kBufferRsrcWord3 = 0x00020000;

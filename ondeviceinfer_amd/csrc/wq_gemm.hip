@@ -168,7 +168,8 @@ template <GFmt F, int NT, int MT>
 __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restrict__ x, int M, int K,
                                                          const void* __restrict__ wsrc,
                                                          const void* __restrict__ wmeta, int N, int bpg,
-                                                         const half_t* __restrict__ bias, half_t* __restrict__ y, int rpx) {
+                                                         const half_t* __restrict__ bias, half_t* __restrict__ y, int rpx,
+                                                         int w8_tiled) {
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kRowBytes;
   constexpr int kInstrPerWave = BM * 16 / 64 / 4;   // 1 KiB direct loads per wave per stage
@@ -216,7 +217,11 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
     rm = buf_rsrc(reinterpret_cast<const uint8_t*>(wmeta) + (size_t)tile0 * ngrp * kW4MetaBytes,
                   (int64_t)(ntile - tile0) * ngrp * kW4MetaBytes);
   } else {
-    rw = buf_rsrc(reinterpret_cast<const int8_t*>(wsrc) + (size_t)tile0 * 16 * K, (int64_t)(N - tile0 * 16) * K);
+    // INT8: row-major rows from tile0 * 16 on, or the tiles from tile0 on
+    // (W8Layout); rows / tiles past the end fall outside the buffer (zeros).
+    rw = w8_tiled ? buf_rsrc(reinterpret_cast<const int8_t*>(wsrc) + (size_t)tile0 * nblk * kW8TileBlockBytes,
+                             (int64_t)(ntile - tile0) * nblk * kW8TileBlockBytes)
+                  : buf_rsrc(reinterpret_cast<const int8_t*>(wsrc) + (size_t)tile0 * 16 * K, (int64_t)(N - tile0 * 16) * K);
   }
   auto fetch_w = [&](int blk, WRegs<F, NT>& r) {
     if constexpr (F == GFmt::W4) {
@@ -230,12 +235,14 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
         r.z[t] = __builtin_amdgcn_raw_buffer_load_b32(rm, 32 + (uint32_t)(i >> 3) * 4, mo, 0);
       }
     } else {
-      const uint32_t vo = (uint32_t)(i * K + 16 * kb);
+      const uint32_t vo = w8_tiled ? (uint32_t)lane * 16 : (uint32_t)(i * K + 16 * kb);
+      const uint32_t p1 = w8_tiled ? kW8TileBlockBytes / 2 : 64;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const uint32_t so = (uint32_t)(t * 16 * K + blk * kW8BlockK);
+        const uint32_t so = w8_tiled ? (uint32_t)((t * nblk + blk) * kW8TileBlockBytes)
+                                     : (uint32_t)(t * 16 * K + blk * kW8BlockK);
         r.a[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo, so, kNtPolicy);
-        r.b[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + 64, so, kNtPolicy);
+        r.b[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + p1, so, kNtPolicy);
       }
     }
   };
@@ -295,7 +302,7 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
                                                            const void* __restrict__ wsrc,
                                                            const void* __restrict__ wmeta, int N, int bpg,
                                                            const half_t* __restrict__ bias, half_t* __restrict__ y,
-                                                           int rpx) {
+                                                           int rpx, int w8_tiled) {
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kRowBytes;
   constexpr int kInstrPerWave = BM * 16 / 64 / 4;   // 1 KiB direct loads per wave per stage
@@ -341,7 +348,11 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
     rm = buf_rsrc(reinterpret_cast<const uint8_t*>(wmeta) + (size_t)tile0 * ngrp * kW4MetaBytes,
                   (int64_t)(ntile - tile0) * ngrp * kW4MetaBytes);
   } else {
-    rw = buf_rsrc(reinterpret_cast<const int8_t*>(wsrc) + (size_t)tile0 * 16 * K, (int64_t)(N - tile0 * 16) * K);
+    // INT8: row-major rows from tile0 * 16 on, or the tiles from tile0 on
+    // (W8Layout); rows / tiles past the end fall outside the buffer (zeros).
+    rw = w8_tiled ? buf_rsrc(reinterpret_cast<const int8_t*>(wsrc) + (size_t)tile0 * nblk * kW8TileBlockBytes,
+                             (int64_t)(ntile - tile0) * nblk * kW8TileBlockBytes)
+                  : buf_rsrc(reinterpret_cast<const int8_t*>(wsrc) + (size_t)tile0 * 16 * K, (int64_t)(N - tile0 * 16) * K);
   }
   // Blocks past the end take an offset beyond every buffer's range, so they
   // read zeros without touching memory.
@@ -359,12 +370,15 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
         r.z[t] = __builtin_amdgcn_raw_buffer_load_b32(rm, 32 + (uint32_t)(i >> 3) * 4, mo, 0);
       }
     } else {
-      const uint32_t vo = (uint32_t)(i * K + 16 * kb);
+      const uint32_t vo = w8_tiled ? (uint32_t)lane * 16 : (uint32_t)(i * K + 16 * kb);
+      const uint32_t p1 = w8_tiled ? kW8TileBlockBytes / 2 : 64;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const uint32_t so = live ? (uint32_t)(t * 16 * K + blk * kW8BlockK) : kPastEnd;
+        const uint32_t so = !live ? kPastEnd
+                            : w8_tiled ? (uint32_t)((t * nblk + blk) * kW8TileBlockBytes)
+                                       : (uint32_t)(t * 16 * K + blk * kW8BlockK);
         r.a[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo, so, kNtPolicy);
-        r.b[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + 64, so, kNtPolicy);
+        r.b[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + p1, so, kNtPolicy);
       }
     }
   };
@@ -417,21 +431,21 @@ int xcd_rows(int M, unsigned grid_y) {
 
 template <GFmt F, int NT, int MT>
 int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
-                const half_t* bias, half_t* y, hipStream_t s) {
+                const half_t* bias, half_t* y, hipStream_t s, int w8_tiled) {
   const int ntile = (N + 15) / 16;
   const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)));
   hipLaunchKernelGGL((wq_gemm_kernel<F, NT, MT>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y,
-                     xcd_rows<F>(M, grid.y));
+                     xcd_rows<F>(M, grid.y), w8_tiled);
   return check_launch(F == GFmt::W4 ? "w4_gemm" : "w8_gemm");
 }
 
 template <GFmt F, int NT, int MT, int D>
 int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
-                     const half_t* bias, half_t* y, hipStream_t s) {
+                     const half_t* bias, half_t* y, hipStream_t s, int w8_tiled) {
   const int ntile = (N + 15) / 16;
   const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)));
   hipLaunchKernelGGL((wq_gemm_deep_kernel<F, NT, MT, D>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y,
-                     xcd_rows<F>(M, grid.y));
+                     xcd_rows<F>(M, grid.y), w8_tiled);
   return check_launch(F == GFmt::W4 ? "w4_gemm_deep" : "w8_gemm_deep");
 }
 
@@ -447,18 +461,20 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
 // tiles.
 template <GFmt F>
 int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
-                     const half_t* bias, half_t* y, hipStream_t s) {
+                     const half_t* bias, half_t* y, hipStream_t s, int w8_tiled) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128;
-  if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
+  if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
   if constexpr (F == GFmt::W4) {
     constexpr long kMinGrid = 384;
     const long mb64 = (M + 63) / 64;
-    if (((ntile + 7) / 8) * mb64 >= kMinGrid) return launch_gemm<F, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
-    if (((ntile + 3) / 4) * mb64 >= kMinGrid) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
-    return launch_gemm_deep<F, 1, 2, 6>(x, M, K, w, meta, N, bpg, bias, y, s);
+    if (((ntile + 7) / 8) * mb64 >= kMinGrid)
+      return launch_gemm<F, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
+    if (((ntile + 3) / 4) * mb64 >= kMinGrid)
+      return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
+    return launch_gemm_deep<F, 1, 2, 6>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
   } else {
-    if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s);
-    return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s);
+    if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
+    return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
   }
 }
 
@@ -466,7 +482,7 @@ int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* m
 
 int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
                    hipStream_t s) {
-  return launch_gemm_auto<GFmt::W4>(x, M, K, tiles, meta, N, G / kW4BlockK, nullptr, y, s);
+  return launch_gemm_auto<GFmt::W4>(x, M, K, tiles, meta, N, G / kW4BlockK, nullptr, y, s, 0);
 }
 
 // Wide N at 16 < M <= 64: the deep ring keeps five weight blocks per wave in
@@ -481,15 +497,15 @@ int launch_w4_gemm_small(const half_t* x, int M, int K, const uint4_t* tiles, co
   const int bpg = G / kW4BlockK;
   const int ntile = (N + 15) / 16;
   if (M <= 32) {
-    if (ntile >= 4096) return launch_gemm_deep<GFmt::W4, 2, 2, 6>(x, M, K, tiles, meta, N, bpg, nullptr, y, s);
-    return launch_gemm_deep<GFmt::W4, 1, 2, 6>(x, M, K, tiles, meta, N, bpg, nullptr, y, s);
+    if (ntile >= 4096) return launch_gemm_deep<GFmt::W4, 2, 2, 6>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
+    return launch_gemm_deep<GFmt::W4, 1, 2, 6>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
   }
-  return launch_gemm_deep<GFmt::W4, 2, 4, 5>(x, M, K, tiles, meta, N, bpg, nullptr, y, s);
+  return launch_gemm_deep<GFmt::W4, 2, 4, 5>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
 }
 
 int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
-                   half_t* y, hipStream_t s) {
-  return launch_gemm_auto<GFmt::W8>(x, M, K, q, scale, N, 1, bias, y, s);
+                   half_t* y, hipStream_t s, int tiled) {
+  return launch_gemm_auto<GFmt::W8>(x, M, K, q, scale, N, 1, bias, y, s, tiled);
 }
 
 }  // namespace wq

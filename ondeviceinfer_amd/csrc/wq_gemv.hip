@@ -265,19 +265,19 @@ __global__ __launch_bounds__(64 * KSW) void w8_skinny_kernel(const half_t* __res
                                                              const int8_t* __restrict__ q,
                                                              const half_t* __restrict__ scale,
                                                              const half_t* __restrict__ bias, int N,
-                                                             half_t* __restrict__ y) {
+                                                             half_t* __restrict__ y, W8Layout wl8) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, kb = lane >> 4;
   const int ntile = (N + 15) >> 4;
   const int nblk = K / kW8BlockK;
   const int b_lo = (wave * nblk) / KSW, b_hi = ((wave + 1) * nblk) / KSW;
+  const int blk_bytes = wl8.block_bytes(), p1 = wl8.piece1();
 
   const int8_t* rowp[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    const int tt = min((int)blockIdx.x * TPW + t, ntile - 1);
-    const int row = min(tt * 16 + i, N - 1);   // rows past N read a valid row; never stored
-    rowp[t] = q + (size_t)row * K + 16 * kb;
+    const int tt = min((int)blockIdx.x * TPW + t, ntile - 1);   // tiles (rows) past the end: read, never stored
+    rowp[t] = q + wl8.lane_base(tt, lane, N, K);
   }
 
   float4_t acc[MC][TPW];
@@ -295,8 +295,8 @@ __global__ __launch_bounds__(64 * KSW) void w8_skinny_kernel(const half_t* __res
       if (blk < b_hi) {
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
-          wa[u][t] = *reinterpret_cast<const uint4_t*>(rowp[t] + blk * kW8BlockK);
-          wb[u][t] = *reinterpret_cast<const uint4_t*>(rowp[t] + blk * kW8BlockK + 64);
+          wa[u][t] = *reinterpret_cast<const uint4_t*>(rowp[t] + (size_t)blk * blk_bytes);
+          wb[u][t] = *reinterpret_cast<const uint4_t*>(rowp[t] + (size_t)blk * blk_bytes + p1);
         }
 #pragma unroll
         for (int mc = 0; mc < MC; ++mc) {
@@ -375,6 +375,8 @@ __global__ __launch_bounds__(64 * KSW) void w8_skinny_kernel(const half_t* __res
 // 1152+q and takes 1152 * x off with a constant fragment.  Rows m >= M read row M-1
 // (in bounds) and are never stored; reads past the end of x are clamped.
 enum class WFmt { W4, W8 };
+// The flat kernel's fmt_arg: W4 = log2 of the 128-k blocks per group; W8 =
+// the weight layout (W8Layout::tiled: 1 INT8 tiles, 0 row-major [N, K]).
 
 // Widest workgroup (in waves) each instantiation is compiled for: the
 // register budget of a 1024-thread group (128 VGPRs) holds about 12 W4 or 8
@@ -445,7 +447,7 @@ __device__ __forceinline__ uint4_t silu_mul8(uint4_t gv, uint4_t uv) {
 template <int NB, int MM, WFmt F, XMode XM = XMode::Plain>
 __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F>())) void gemv_flat_kernel(
     const half_t* __restrict__ x, int M, int K, const void* __restrict__ wsrc, const void* __restrict__ wmeta,
-    const half_t* __restrict__ bias, int N, int g_shift, half_t* y, int S,
+    const half_t* __restrict__ bias, int N, int fmt_arg, half_t* y, int S,
     float4_t* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt, FuseArgs fz) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int NBX = NB + 1;                                // staged slice length (blocks)
@@ -513,9 +515,9 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
   int g_lo = 0;
   uint2_t mr[kMPerLane > 0 ? kMPerLane : 1];
   if constexpr (F == WFmt::W4) {
-    const int ngrp = nblk >> g_shift;
-    g_lo = b0 >> g_shift;
-    const int g_hi = min((b0 + NB) >> g_shift, ngrp - 1);
+    const int ngrp = nblk >> fmt_arg;
+    g_lo = b0 >> fmt_arg;
+    const int g_hi = min((b0 + NB) >> fmt_arg, ngrp - 1);
     const int meta_chunks = (g_hi - g_lo + 1) * (kW4MetaBytes / 8);
     const uint2_t* mg = reinterpret_cast<const uint2_t*>(reinterpret_cast<const uint8_t*>(wmeta) +
                                                          ((size_t)tile * ngrp + g_lo) * kW4MetaBytes);
@@ -529,16 +531,19 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
   if constexpr (F == WFmt::W4) {
     wp = reinterpret_cast<const uint4_t*>(wsrc) + ((size_t)tile * nblk + b0) * 64 + lane;
   } else {
-    const int row = min(tile * 16 + i, N - 1);
-    wp = reinterpret_cast<const uint4_t*>(reinterpret_cast<const int8_t*>(wsrc) + (size_t)row * K +
-                                          (size_t)b0 * kW8BlockK + 16 * kb);
+    const W8Layout wl8{fmt_arg};
+    wp = reinterpret_cast<const uint4_t*>(reinterpret_cast<const int8_t*>(wsrc) + wl8.lane_base(tile, lane, N, K) +
+                                          (size_t)b0 * wl8.block_bytes());
   }
+  // INT8: a block and piece 1 in 16-byte units (row-major 8 / 4, tiles 128 / 64).
+  const int w8_blk = F == WFmt::W8 ? W8Layout{fmt_arg}.block_bytes() / 16 : 0;
+  const int w8_p1 = F == WFmt::W8 ? W8Layout{fmt_arg}.piece1() / 16 : 0;
   auto load_block = [&](BlockRegs<F>& r, int s2) {
     if constexpr (F == WFmt::W4) {
       r.w = __builtin_nontemporal_load(wp + s2 * 64);
     } else {
-      r.a = __builtin_nontemporal_load(wp + s2 * 8);
-      r.b = __builtin_nontemporal_load(wp + s2 * 8 + 4);
+      r.a = __builtin_nontemporal_load(wp + s2 * w8_blk);
+      r.b = __builtin_nontemporal_load(wp + s2 * w8_blk + w8_p1);
     }
   };
   BlockRegs<F> ring[D], xtra;
@@ -580,7 +585,7 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
       for (int w = 0; w < 4; ++w) xv[w] = ld_h8(xp + blk_kcol<F>(kb, w));
     }
     if constexpr (F == WFmt::W4) {
-      const uint8_t* rec = ml + (((b0 + s2) >> g_shift) - g_lo) * kW4MetaBytes;
+      const uint8_t* rec = ml + (((b0 + s2) >> fmt_arg) - g_lo) * kW4MetaBytes;
       const uint2_t sc = *reinterpret_cast<const uint2_t*>(rec + 8 * kb);
       const uint32_t zw = *reinterpret_cast<const uint32_t*>(rec + 32 + 4 * (i >> 3));
       // The zero-point terms go through the matrix pipe (they need only x
@@ -793,27 +798,27 @@ int launch_w4_skinny_k(int ksw, const half_t* x, int M, int K, const uint4_t* ti
 
 template <int MC, int TPW, int KSW>
 int launch_w8_skinny_cfg(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias,
-                         int N, half_t* y, hipStream_t s) {
+                         int N, half_t* y, hipStream_t s, int tiled) {
   const int ntile = (N + 15) / 16;
   const unsigned grid = (unsigned)((ntile + TPW - 1) / TPW);
-  hipLaunchKernelGGL((w8_skinny_kernel<MC, TPW, KSW, skinny_unroll<MC>()>), dim3(grid), dim3(64 * KSW), 0, s, x, M, K, q, scale, bias,
-                     N, y);
+  hipLaunchKernelGGL((w8_skinny_kernel<MC, TPW, KSW, skinny_unroll<MC>()>), dim3(grid), dim3(64 * KSW), 0, s, x, M, K,
+                     q, scale, bias, N, y, W8Layout{tiled});
   return check_launch("w8_skinny");
 }
 
 template <int MC, int TPW>
 int launch_w8_skinny_k(int ksw, const half_t* x, int M, int K, const int8_t* q, const half_t* scale,
-                       const half_t* bias, int N, half_t* y, hipStream_t s) {
+                       const half_t* bias, int N, half_t* y, hipStream_t s, int tiled) {
   switch (ksw) {
-    case 1: return launch_w8_skinny_cfg<MC, TPW, 1>(x, M, K, q, scale, bias, N, y, s);
-    case 2: return launch_w8_skinny_cfg<MC, TPW, 2>(x, M, K, q, scale, bias, N, y, s);
-    case 4: return launch_w8_skinny_cfg<MC, TPW, 4>(x, M, K, q, scale, bias, N, y, s);
+    case 1: return launch_w8_skinny_cfg<MC, TPW, 1>(x, M, K, q, scale, bias, N, y, s, tiled);
+    case 2: return launch_w8_skinny_cfg<MC, TPW, 2>(x, M, K, q, scale, bias, N, y, s, tiled);
+    case 4: return launch_w8_skinny_cfg<MC, TPW, 4>(x, M, K, q, scale, bias, N, y, s, tiled);
     default:
       if constexpr (skinny_max_ksw<MC, TPW>() >= 16) {
-        if (ksw == 8) return launch_w8_skinny_cfg<MC, TPW, 8>(x, M, K, q, scale, bias, N, y, s);
-        return launch_w8_skinny_cfg<MC, TPW, 16>(x, M, K, q, scale, bias, N, y, s);
+        if (ksw == 8) return launch_w8_skinny_cfg<MC, TPW, 8>(x, M, K, q, scale, bias, N, y, s, tiled);
+        return launch_w8_skinny_cfg<MC, TPW, 16>(x, M, K, q, scale, bias, N, y, s, tiled);
       } else {
-        return launch_w8_skinny_cfg<MC, TPW, 4>(x, M, K, q, scale, bias, N, y, s);
+        return launch_w8_skinny_cfg<MC, TPW, 4>(x, M, K, q, scale, bias, N, y, s, tiled);
       }
   }
 }
@@ -863,7 +868,7 @@ size_t flat_workspace_bytes(int ntile, int split) {
 
 template <int NB, int MM, WFmt F, XMode XM>
 int launch_flat(const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias, int N,
-                int g_shift, half_t* y, FlatPlan p, void* ws, const FuseArgs& fz, hipStream_t s) {
+                int fmt_arg, half_t* y, FlatPlan p, void* ws, const FuseArgs& fz, hipStream_t s) {
   if (p.ksw > flat_max_ksw<NB, F>()) return kNotApplicable;
   const int lds = flat_lds_bytes<NB, MM, F>(p.ksw);
   if (lds > kGemvMaxBytes) return kNotApplicable;
@@ -873,24 +878,24 @@ int launch_flat(const half_t* x, int M, int K, const void* w, const void* meta, 
                                                              (((size_t)ntile * 4 + 255) & ~(size_t)255))
                                : nullptr;
   hipLaunchKernelGGL((gemv_flat_kernel<NB, MM, F, XM>), dim3((unsigned)ntile, (unsigned)p.split), dim3(64 * p.ksw),
-                     lds, s, x, M, K, w, meta, bias, N, g_shift, y, p.split, part, cnt, fz);
+                     lds, s, x, M, K, w, meta, bias, N, fmt_arg, y, p.split, part, cnt, fz);
   return check_launch(F == WFmt::W4 ? "w4_gemv_flat" : "w8_gemv_flat");
 }
 
 template <int MM, WFmt F, XMode XM, int NB = 1>
 int launch_flat_nb(int nb, const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias,
-                   int N, int g_shift, half_t* y, FlatPlan p, void* ws, const FuseArgs& fz, hipStream_t s) {
+                   int N, int fmt_arg, half_t* y, FlatPlan p, void* ws, const FuseArgs& fz, hipStream_t s) {
   if constexpr (NB > kFlatMaxNB) {
     return kNotApplicable;
   } else {
-    if (nb == NB) return launch_flat<NB, MM, F, XM>(x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
-    return launch_flat_nb<MM, F, XM, NB + 1>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
+    if (nb == NB) return launch_flat<NB, MM, F, XM>(x, M, K, w, meta, bias, N, fmt_arg, y, p, ws, fz, s);
+    return launch_flat_nb<MM, F, XM, NB + 1>(nb, x, M, K, w, meta, bias, N, fmt_arg, y, p, ws, fz, s);
   }
 }
 
 template <WFmt F>
 int launch_gemv_flat(const half_t* x, int M, int K, const void* w, const void* meta, const half_t* bias, int N,
-                     int g_shift, half_t* y, void* ws, size_t ws_bytes, hipStream_t s,
+                     int fmt_arg, half_t* y, void* ws, size_t ws_bytes, hipStream_t s,
                      XMode xm = XMode::Plain, const FuseArgs& fz = FuseArgs{}) {
   const int nblk = K / kW4BlockK, ntile = (N + 15) / 16;
   FlatPlan p = plan_flat<F>(ntile, nblk);
@@ -899,10 +904,10 @@ int launch_gemv_flat(const half_t* x, int M, int K, const void* w, const void* m
     p = plan_flat<F>(ntile, nblk, false);
   const int nb = (nblk / p.split) / p.ksw;
   if (nb < 1 || nb > kFlatMaxNB) return kNotApplicable;
-  if (xm == XMode::RmsNorm) return launch_flat_nb<1, F, XMode::RmsNorm>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
-  if (xm == XMode::SiluMul) return launch_flat_nb<1, F, XMode::SiluMul>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
-  if (M == 1) return launch_flat_nb<1, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
-  return launch_flat_nb<4, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, g_shift, y, p, ws, fz, s);
+  if (xm == XMode::RmsNorm) return launch_flat_nb<1, F, XMode::RmsNorm>(nb, x, M, K, w, meta, bias, N, fmt_arg, y, p, ws, fz, s);
+  if (xm == XMode::SiluMul) return launch_flat_nb<1, F, XMode::SiluMul>(nb, x, M, K, w, meta, bias, N, fmt_arg, y, p, ws, fz, s);
+  if (M == 1) return launch_flat_nb<1, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, fmt_arg, y, p, ws, fz, s);
+  return launch_flat_nb<4, F, XMode::Plain>(nb, x, M, K, w, meta, bias, N, fmt_arg, y, p, ws, fz, s);
 }
 
 int launch_w4_gemv_flat(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
@@ -932,10 +937,10 @@ int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uin
 int launch_w8_gemv_fused(const half_t* x, int K, const int8_t* q, const half_t* scale, int N, int x_mode,
                          const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
                          const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
-                         hipStream_t s) {
+                         hipStream_t s, int tiled) {
   const FuseArgs fz{norm_w, sumsq_in, sumsq_count, eps, residual, sumsq_out};
   const XMode xm = x_mode == 1 ? XMode::RmsNorm : x_mode == 2 ? XMode::SiluMul : XMode::Plain;
-  const int rc = launch_gemv_flat<WFmt::W8>(x, 1, K, q, scale, nullptr, N, 0, y, ws, ws_bytes, s, xm, fz);
+  const int rc = launch_gemv_flat<WFmt::W8>(x, 1, K, q, scale, nullptr, N, tiled, y, ws, ws_bytes, s, xm, fz);
   if (rc == kNotApplicable)
     return fail(WQ_ERR_UNSUPPORTED, "fused decode linear: this k is beyond the decode kernel's blocks per wave");
   return rc;
@@ -970,18 +975,18 @@ int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const 
 }
 
 int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
-                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s) {
+                     half_t* y, void* ws, size_t ws_bytes, hipStream_t s, int tiled) {
   if (M <= kGemvFlatMaxM) {
-    int rc = launch_gemv_flat<WFmt::W8>(x, M, K, q, scale, bias, N, 0, y, ws, ws_bytes, s);
+    int rc = launch_gemv_flat<WFmt::W8>(x, M, K, q, scale, bias, N, tiled, y, ws, ws_bytes, s);
     if (rc != kNotApplicable) return rc;
   }
   const int mc = (M + 15) / 16;
   const SkinnyCfg c = pick_skinny((N + 15) / 16, K / kW8BlockK, mc, false);
   switch (mc) {
-    case 1: return launch_w8_skinny_k<1, 1>(c.ksw, x, M, K, q, scale, bias, N, y, s);
-    case 2: return launch_w8_skinny_k<2, 2>(c.ksw, x, M, K, q, scale, bias, N, y, s);
-    case 3: return launch_w8_skinny_k<3, 2>(c.ksw, x, M, K, q, scale, bias, N, y, s);
-    default: return launch_w8_skinny_k<4, 2>(c.ksw, x, M, K, q, scale, bias, N, y, s);
+    case 1: return launch_w8_skinny_k<1, 1>(c.ksw, x, M, K, q, scale, bias, N, y, s, tiled);
+    case 2: return launch_w8_skinny_k<2, 2>(c.ksw, x, M, K, q, scale, bias, N, y, s, tiled);
+    case 3: return launch_w8_skinny_k<3, 2>(c.ksw, x, M, K, q, scale, bias, N, y, s, tiled);
+    default: return launch_w8_skinny_k<4, 2>(c.ksw, x, M, K, q, scale, bias, N, y, s, tiled);
   }
 }
 

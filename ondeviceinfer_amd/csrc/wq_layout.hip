@@ -8,6 +8,11 @@
 // load, and each word converts to four fp16 pairs with one AND-OR apiece.
 // meta holds, per (tile, group), the 16 fp16 scales of the tile's rows and
 // the two zero-point words of those rows (40 bytes).
+//
+// INT8 tile layout: one 2 KiB block per (16-row tile, 128-k block), two
+// 1 KiB pieces of 16 bytes per lane in the order the INT8 kernels take them
+// (W8Layout in wq_common.h); the rows are still scaled per row by the
+// caller's fp16 / fp32 scale vector.
 #include "wq_common.h"
 #include "wq_status.h"
 
@@ -55,6 +60,34 @@ __global__ void w4_repack_tiles_kernel(const uint32_t* __restrict__ packed, int6
     out.w = nibble_order_from_natural(src.w);
   }
   tiles[idx] = out;
+}
+
+// INT8 tiles (W8Layout in wq_common.h): one thread per (tile, block, piece,
+// lane) moves the lane's 16 bytes; rows past n are written as zeros.
+__global__ void w8_repack_kernel(const int8_t* __restrict__ q, int64_t n, int64_t k, int64_t nblk, int64_t total,
+                                 uint4_t* __restrict__ tiles) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int lane = (int)(idx & 63), piece = (int)((idx >> 6) & 1);
+  const int64_t tb = idx >> 7;           // tile * nblk + blk
+  const int64_t t = tb / nblk, blk = tb - t * nblk;
+  const int64_t row = t * 16 + (lane & 15);
+  uint4_t v = {0u, 0u, 0u, 0u};
+  if (row < n)
+    v = *reinterpret_cast<const uint4_t*>(q + row * k + blk * kW8BlockK + 64 * piece + 16 * (lane >> 4));
+  tiles[idx] = v;
+}
+
+__global__ void w8_unpack_kernel(const uint4_t* __restrict__ tiles, int64_t n, int64_t k, int64_t nblk,
+                                 int64_t total, int8_t* __restrict__ q) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int lane = (int)(idx & 63), piece = (int)((idx >> 6) & 1);
+  const int64_t tb = idx >> 7;
+  const int64_t t = tb / nblk, blk = tb - t * nblk;
+  const int64_t row = t * 16 + (lane & 15);
+  if (row < n)
+    *reinterpret_cast<uint4_t*>(q + row * k + blk * kW8BlockK + 64 * piece + 16 * (lane >> 4)) = tiles[idx];
 }
 
 // One thread per (tile, group): 16 scales + 2 zero words.
@@ -384,6 +417,43 @@ extern "C" int wq_w4_decode_rows(const int32_t* weight_packed, const float* weig
                      reinterpret_cast<const uint32_t*>(weight_zero_point), rows, num_rows, n, k, num_groups,
                      group_size, weight);
   return check_launch("w4_decode_rows");
+}
+
+extern "C" int wq_w8_tiles_size(int64_t n, int64_t k, size_t* bytes) {
+  WQ_REQUIRE(n > 0 && k > 0, WQ_ERR_INVALID_ARGUMENT, "non-positive shape n=%lld k=%lld", (long long)n,
+             (long long)k);
+  WQ_REQUIRE(k % kW8BlockK == 0, WQ_ERR_UNSUPPORTED, "INT8 tiles need k %% 128 == 0 (k=%lld)", (long long)k);
+  WQ_REQUIRE(bytes, WQ_ERR_INVALID_ARGUMENT, "null size output");
+  *bytes = (size_t)ceil_div(n, 16) * (size_t)(k / kW8BlockK) * kW8TileBlockBytes;
+  return WQ_OK;
+}
+
+extern "C" int wq_w8_repack(const int8_t* qweight, int64_t n, int64_t k, void* tiles, void* stream) {
+  size_t bytes = 0;
+  if (int st = wq_w8_tiles_size(n, k, &bytes)) return st;
+  WQ_REQUIRE(qweight && tiles, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(((reinterpret_cast<uintptr_t>(qweight) | reinterpret_cast<uintptr_t>(tiles)) & 15u) == 0,
+             WQ_ERR_INVALID_ARGUMENT, "qweight and tiles must be 16-byte aligned");
+  const int64_t total = (int64_t)(bytes / 16);
+  int64_t blocks;
+  if (launch_1d(total, 256, blocks)) return fail(WQ_ERR_UNSUPPORTED, "repack grid too large");
+  hipLaunchKernelGGL(w8_repack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), qweight, n, k,
+                     k / kW8BlockK, total, reinterpret_cast<uint4_t*>(tiles));
+  return check_launch("w8_repack");
+}
+
+extern "C" int wq_w8_unpack(const void* tiles, int64_t n, int64_t k, int8_t* qweight, void* stream) {
+  size_t bytes = 0;
+  if (int st = wq_w8_tiles_size(n, k, &bytes)) return st;
+  WQ_REQUIRE(qweight && tiles, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(((reinterpret_cast<uintptr_t>(qweight) | reinterpret_cast<uintptr_t>(tiles)) & 15u) == 0,
+             WQ_ERR_INVALID_ARGUMENT, "qweight and tiles must be 16-byte aligned");
+  const int64_t total = (int64_t)(bytes / 16);
+  int64_t blocks;
+  if (launch_1d(total, 256, blocks)) return fail(WQ_ERR_UNSUPPORTED, "unpack grid too large");
+  hipLaunchKernelGGL(w8_unpack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint4_t*>(tiles), n, k, k / kW8BlockK, total, qweight);
+  return check_launch("w8_unpack");
 }
 
 extern "C" int wq_w8_decode(const int8_t* qweight, const float* scale, int64_t n, int64_t k, uint16_t* weight,

@@ -85,23 +85,25 @@ __device__ __forceinline__ void w8a8_store(int32_t acc, int m, int n, const floa
 __global__ __launch_bounds__(1024) void w8a8_gemv_kernel(const int8_t* __restrict__ qx, const float* __restrict__ sx,
                                                          int M, int K, const int8_t* __restrict__ qw,
                                                          const float* __restrict__ sw, const half_t* __restrict__ bias,
-                                                         int N, half_t* __restrict__ y) {
+                                                         int N, half_t* __restrict__ y, W8Layout wl8) {
   __shared__ int4v_t red[16][64];
   const int ksw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i = lane & 15, kb = lane >> 4;
   const int tile = blockIdx.x;
   const int nsteps = K / kI8Step;
   const int s_lo = (wave * nsteps) / ksw, s_hi = ((wave + 1) * nsteps) / ksw;
-  const int8_t* wp = qw + (size_t)min(tile * 16 + i, N - 1) * K + 16 * kb;
+  const int8_t* wp = qw + wl8.lane_base(tile, lane, N, K);
   const int8_t* xp = qx + (size_t)min(i, M - 1) * K + 16 * kb;
+  const int blk_bytes = wl8.block_bytes(), p1 = wl8.piece1();
   int4v_t acc = {0, 0, 0, 0};
   for (int s0 = s_lo; s0 < s_hi; s0 += 8) {
     uint4_t a[8], b[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const size_t off = (size_t)kI8Step * min(s0 + j, s_hi - 1);
-      a[j] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t*>(wp + off));
-      b[j] = *reinterpret_cast<const uint4_t*>(xp + off);
+      const int st = min(s0 + j, s_hi - 1);   // 64-k step: block st / 2, piece st % 2
+      a[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint4_t*>(wp + (size_t)(st >> 1) * blk_bytes + (st & 1) * p1));
+      b[j] = *reinterpret_cast<const uint4_t*>(xp + (size_t)kI8Step * st);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
                                                            const int8_t* __restrict__ qw,
                                                            const float* __restrict__ sw,
                                                            const half_t* __restrict__ bias, int N,
-                                                           half_t* __restrict__ y) {
+                                                           half_t* __restrict__ y, W8Layout wl8) {
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kI8RowBytes;
   constexpr int kInstrPerWave = kStageBytes / 1024 / 4;   // 1 KiB per wave-wide DMA instruction
@@ -168,7 +170,8 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
   const int tile0 = ((int)blockIdx.x * 4 + wave) * NT;
   const int8_t* wrow[NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) wrow[t] = qw + (size_t)min(min(tile0 + t, ntile - 1) * 16 + i, N - 1) * K + 16 * kb;
+  for (int t = 0; t < NT; ++t) wrow[t] = qw + wl8.lane_base(min(tile0 + t, ntile - 1), lane, N, K);
+  const int blk_bytes = wl8.block_bytes(), p1 = wl8.piece1();
 
   // Stage `st` <- x rows m0 .. m0+BM-1, k block `blk`: instruction J of the
   // workgroup fills bytes [1024 J, 1024 J + 1024), i.e. rows 8J .. 8J+7;
@@ -187,9 +190,9 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
   auto fetch_w = [&](int blk, uint4_t (&r)[NT][2]) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const uint4_t* p = reinterpret_cast<const uint4_t*>(wrow[t] + (size_t)blk * kI8Blk);
-      r[t][0] = p[0];   // k + 16 kb .. +15
-      r[t][1] = p[4];   // k + 64 + 16 kb .. +15
+      const int8_t* p = wrow[t] + (size_t)blk * blk_bytes;
+      r[t][0] = *reinterpret_cast<const uint4_t*>(p);        // k + 16 kb .. +15
+      r[t][1] = *reinterpret_cast<const uint4_t*>(p + p1);   // k + 64 + 16 kb .. +15
     }
   };
 
@@ -268,13 +271,17 @@ extern "C" int wq_w8a8_quantize(const uint16_t* x, int64_t m, int64_t k, int8_t*
   return check_launch("w8a8_quantize");
 }
 
-extern "C" int wq_w8a8_linear(const int8_t* qx, const float* x_scale, int64_t m, int64_t k, const int8_t* qweight,
-                              const float* w_scale, int64_t n, const uint16_t* bias, uint16_t* y, void* stream) {
+namespace {
+
+int w8a8_linear_impl(const int8_t* qx, const float* x_scale, int64_t m, int64_t k, const int8_t* qweight,
+                     const float* w_scale, int64_t n, const uint16_t* bias, uint16_t* y, void* stream, int tiled) {
   if (m == 0 || n == 0) return WQ_OK;
   WQ_REQUIRE(qx && x_scale && qweight && w_scale && y, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
   WQ_REQUIRE(m > 0 && n > 0 && k > 0 && m <= 0x7fffffff && n <= 0x7fffffff && k <= (1 << 26),
              WQ_ERR_INVALID_ARGUMENT, "m, n, k out of range");
-  WQ_REQUIRE(k % kI8Step == 0, WQ_ERR_UNSUPPORTED, "W8A8 linear needs k %% 64 == 0 (got %lld)", (long long)k);
+  WQ_REQUIRE(k % (tiled ? kI8Blk : kI8Step) == 0, WQ_ERR_UNSUPPORTED, "W8A8 linear needs k %% %d == 0 (got %lld)",
+             tiled ? kI8Blk : kI8Step, (long long)k);
+  const W8Layout wl8{tiled};
   WQ_REQUIRE(((uintptr_t)qx | (uintptr_t)qweight) % 16 == 0, WQ_ERR_INVALID_ARGUMENT,
              "qx and qweight must be 16-byte aligned");
   const half_t* b = reinterpret_cast<const half_t*>(bias);
@@ -291,7 +298,7 @@ extern "C" int wq_w8a8_linear(const int8_t* qx, const float* x_scale, int64_t m,
     const dim3 grid((unsigned)((ntile + 4 * nt - 1) / (4 * nt)), (unsigned)mblocks);
     auto launch = [&](auto kernel) {
       hipLaunchKernelGGL(kernel, grid, dim3(256), 0, as_stream(stream), qx, x_scale, (int)m, (int)k, qweight,
-                         w_scale, b, (int)n, yy);
+                         w_scale, b, (int)n, yy, wl8);
     };
     if (big_m) {
       if (nt == 4) launch(w8a8_gemm_kernel<4, 8>); else launch(w8a8_gemm_kernel<1, 8>);
@@ -306,9 +313,21 @@ extern "C" int wq_w8a8_linear(const int8_t* qx, const float* x_scale, int64_t m,
   for (int64_t r = 0; r < m; r += kW8A8GemvMaxM) {   // batches beyond 16 rows only when k % 128 != 0
     const int64_t mr = m - r < kW8A8GemvMaxM ? m - r : kW8A8GemvMaxM;
     hipLaunchKernelGGL(w8a8_gemv_kernel, dim3((unsigned)ntile), dim3(64 * ksw), 0, as_stream(stream), qx + r * k,
-                       x_scale + r, (int)mr, (int)k, qweight, w_scale, b, (int)n, yy + r * n);
+                       x_scale + r, (int)mr, (int)k, qweight, w_scale, b, (int)n, yy + r * n, wl8);
     const int rc = check_launch("w8a8_gemv");
     if (rc != WQ_OK) return rc;
   }
   return WQ_OK;
+}
+
+}  // namespace
+
+extern "C" int wq_w8a8_linear(const int8_t* qx, const float* x_scale, int64_t m, int64_t k, const int8_t* qweight,
+                              const float* w_scale, int64_t n, const uint16_t* bias, uint16_t* y, void* stream) {
+  return w8a8_linear_impl(qx, x_scale, m, k, qweight, w_scale, n, bias, y, stream, 0);
+}
+
+extern "C" int wq_w8a8_linear_tiled(const int8_t* qx, const float* x_scale, int64_t m, int64_t k, const void* tiles,
+                                    const float* w_scale, int64_t n, const uint16_t* bias, uint16_t* y, void* stream) {
+  return w8a8_linear_impl(qx, x_scale, m, k, reinterpret_cast<const int8_t*>(tiles), w_scale, n, bias, y, stream, 1);
 }

@@ -71,6 +71,11 @@ def int8_weight_only_linear(inputs: Tensor, weights: Mapping[str, Tensor], weigh
     n, k = qweight.shape
     x = inputs.reshape(-1, k)
     scale16 = scale if scale.dtype == torch.float16 else scale.half()
+    # A layer bound for the decode graph (_bind_int8_v1) also holds the same
+    # weight as INT8 tiles, which the kernels stream faster; same results.
+    prepared = weights.get(weight_name.removesuffix('.weight') + '._prepared')
+    if prepared is not None and prepared.n == n and prepared.k == k:
+        qweight, scale16 = prepared.qweight, prepared.scale
     with nvtx_range(f'w8a16_linear::{weight_name}'):
         if stats is not None and stats.enabled and inputs.device.type == 'cuda':
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -187,24 +192,27 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
 
 def _bind_int8_v1(layer: dict, ops) -> None:
     """Give an INT8 v1 layer the prepared entries the decode graph runs:
-    per linear a ``PreparedW8`` over its ``qweight`` / fp16 ``scale``, then
-    q|k|v and gate|up concatenated (``fuse_projections``), after which the
-    parts' ``qweight`` / ``scale`` entries are rebound to views of the fused
-    copies so that no weight is held twice.  Values are unchanged, so the
-    eager ``int8_weight_only_linear`` path reads the same weights."""
-    from .weight_quantization.backend import PreparedW8
+    per linear a ``PreparedW8`` over its weight as INT8 tiles (``int8_streamed``)
+    and fp16 ``scale``, then q|k|v and gate|up concatenated
+    (``fuse_projections``).  The row-major ``qweight`` / ``scale`` entries
+    stay as the reference keeps them; ``int8_weight_only_linear`` takes the
+    tiles of a bound layer (same values, same results).  When the weights
+    stay row-major (k % 128 != 0) the parts' entries are rebound to views of
+    the fused copies so that no weight is held twice."""
+    from .weight_quantization.backend import PreparedW8, int8_streamed
     if not all(qweight_name(n) in layer for n in LINEAR_WEIGHT_NAMES) or QKV_FUSED.removesuffix('.weight') + \
             '._prepared' in layer:
         return
     for name in LINEAR_WEIGHT_NAMES:
         q = layer[qweight_name(name)]
         s16 = layer[scale_name(name)].reshape(-1).half().contiguous()
-        layer[name.removesuffix('.weight') + '._prepared'] = PreparedW8(q.contiguous(), s16, int(q.shape[1]),
+        layer[name.removesuffix('.weight') + '._prepared'] = PreparedW8(int8_streamed(q), s16, int(q.shape[1]),
                                                                        int(q.shape[0]))
     ops.fuse_projections(layer)
     for name in LINEAR_WEIGHT_NAMES:
         p = layer[name.removesuffix('.weight') + '._prepared']
-        layer[qweight_name(name)] = p.qweight
+        if isinstance(p.qweight, torch.Tensor):
+            layer[qweight_name(name)] = p.qweight
         if layer[scale_name(name)].dtype == torch.float16:
             layer[scale_name(name)] = p.scale
 

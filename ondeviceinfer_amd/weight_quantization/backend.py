@@ -109,17 +109,26 @@ class PreparedW4(NamedTuple):
 
 
 class PreparedW8(NamedTuple):
-    qweight: torch.Tensor     # int8 [N, K] (row-major, consumed as stored)
+    qweight: object           # _native.W8Tiles (k % 128 == 0), else int8 [N, K] row-major as stored
     scale: torch.Tensor       # fp16 [N]
     k: int
     n: int
 
 
 class PreparedW8A8(NamedTuple):
-    qweight: torch.Tensor     # int8 [N, K] (row-major, consumed as stored)
+    qweight: object           # _native.W8Tiles (k % 128 == 0), else int8 [N, K] row-major as stored
     scale: torch.Tensor       # fp32 [N]
     k: int
     n: int
+
+
+def int8_streamed(q: torch.Tensor):
+    """The form the INT8 kernels stream a row-major INT8 weight in: its
+    tiles (``_native.w8_repack``) when k % 128 == 0, which turn every 16-byte
+    lane load into one contiguous 1 KiB wave load (same values, same results),
+    else the tensor itself."""
+    q = q.contiguous()
+    return _native.w8_repack(q) if q.shape[1] % 128 == 0 else q
 
 
 class NativeOps:
@@ -342,22 +351,24 @@ class CompressedLinearBackend:
             if q.dtype != torch.int8:
                 raise TypeError(f'{name}: expected INT8, got {q.dtype}')
             n, k = q.shape
+            # The raw weight stays in the dict, as in the reference (backend.py:227-231).
             if self.name == 'w8a16':
                 scale = layer[prefix + '.weight_scale'].reshape(-1).half().contiguous()
-                layer[prefix + '._prepared'] = PreparedW8(q.contiguous(), scale, k, n)
+                layer[prefix + '._prepared'] = PreparedW8(int8_streamed(q), scale, k, n)
             else:   # the reference keeps the scale in fp32 for the scaled GEMM (backend.py:231)
                 scale = layer[prefix + '.weight_scale'].float().reshape(-1).contiguous()
-                layer[prefix + '._prepared'] = PreparedW8A8(q.contiguous(), scale, k, n)
+                layer[prefix + '._prepared'] = PreparedW8A8(int8_streamed(q), scale, k, n)
 
     def fuse_projections(self, layer: dict) -> None:
         """Add ``self_attn.qkv_proj._prepared`` and ``mlp.gate_up_proj._prepared``:
         the prepared q/k/v (gate/up) weights concatenated along N, so each
         group runs as one linear whose output is ``[q | k | v]``
-        (``[gate | up]``).  W4 tiles and meta are tile-major and INT8 rows are
-        row-major, so concatenation is a plain copy; afterwards the parts'
-        own ``_prepared`` entries are views into the fused buffers (no
-        duplicate weights).  Layers whose parts do not line up (mixed formats,
-        N not a multiple of 16) are left as they are."""
+        (``[gate | up]``).  W4 tiles and meta and INT8 tiles are tile-major
+        and row-major INT8 is row-major, so concatenation is a plain copy;
+        afterwards the parts' own ``_prepared`` entries are views into the
+        fused buffers (no duplicate weights).  Layers whose parts do not line
+        up (mixed formats, tiles with N not a multiple of 16) are left as
+        they are."""
         for fused, parts in FUSED_PROJECTIONS.items():
             preps = [layer.get(p + '._prepared') for p in parts]
             if fused + '._prepared' in layer or any(p is None for p in preps):
@@ -381,13 +392,28 @@ class CompressedLinearBackend:
                 if len({p.k for p in preps}) != 1:
                     continue
                 kind = type(preps[0])
-                q = torch.cat([p.qweight for p in preps])
+                k = preps[0].k
                 sc = torch.cat([p.scale for p in preps])
-                layer[fused + '._prepared'] = kind(q, sc, preps[0].k, int(q.shape[0]))
-                r0 = 0
-                for part, p in zip(parts, preps):
-                    layer[part + '._prepared'] = kind(q[r0:r0 + p.n], sc[r0:r0 + p.n], p.k, p.n)
-                    r0 += p.n
+                n = sum(p.n for p in preps)
+                if all(isinstance(p.qweight, _native.W8Tiles) for p in preps):
+                    if any(p.n % 16 for p in preps):   # the tiles of a part end on a 16-row boundary
+                        continue
+                    tiles = torch.cat([p.qweight.tiles for p in preps])
+                    layer[fused + '._prepared'] = kind(_native.W8Tiles(tiles, n, k), sc, k, n)
+                    t0 = r0 = 0
+                    for part, p in zip(parts, preps):
+                        size = p.qweight.tiles.numel()
+                        layer[part + '._prepared'] = kind(_native.W8Tiles(tiles[t0:t0 + size], p.n, k),
+                                                          sc[r0:r0 + p.n], k, p.n)
+                        t0 += size
+                        r0 += p.n
+                elif all(isinstance(p.qweight, torch.Tensor) for p in preps):
+                    q = torch.cat([p.qweight for p in preps])
+                    layer[fused + '._prepared'] = kind(q, sc, k, n)
+                    r0 = 0
+                    for part, p in zip(parts, preps):
+                        layer[part + '._prepared'] = kind(q[r0:r0 + p.n], sc[r0:r0 + p.n], p.k, p.n)
+                        r0 += p.n
 
     def linear(self, inputs: torch.Tensor, weights: dict, name: str) -> torch.Tensor:
         self.calls += 1

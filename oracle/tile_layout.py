@@ -25,8 +25,15 @@ then the two zero-point words of those rows, copied from
 ``weight_zero_point[2t, g]`` and ``[2t+1, g]`` (``0x88888888`` = z 8 for the
 symmetric uint4b8 format).
 
-INT8 weights have no tile layout: the kernels read them in their stored
-row-major ``[N, K]`` form.
+INT8 layout (K a multiple of 128)
+---------------------------------
+``tiles``: int8 ``[ceil(N/16), K/128, 2, 64, 16]``: per (16-row tile ``t``,
+128-k block ``b``) two 1 KiB pieces; lane ``l`` of piece ``p`` holds
+``q[16t + l%16, 128b + 64p + 16*(l//16) + j]`` for ``j`` in 0..15, the 16 bytes
+the INT8 kernels feed to lane ``l`` (pieces 0 and 1 = the first and second
+64 k of the block).  Rows past N are zero.  The row-major ``[N, K]`` weight
+stays the public form; this one is pinned by ``w8_unpack(w8_repack(q)) == q``
+and by the GPU linears returning the same bits from either form.
 """
 from __future__ import annotations
 
@@ -110,3 +117,23 @@ def w4_dequant(tiles: np.ndarray, meta: np.ndarray, n: int, k: int, group_size: 
     z = unpack_unsigned(zero, 4, 0, n).astype(np.float32)
     groups = np.arange(k) // group_size
     return ((q - z[:, groups]) * scale.astype(np.float32)[:, groups]).astype(np.float16)
+
+
+def w8_repack(q: np.ndarray) -> np.ndarray:
+    """Row-major INT8 ``[N, K]`` -> tiles ``[ceil(N/16), K/128, 2, 64, 16]`` int8."""
+    q = np.asarray(q, dtype=np.int8)
+    n, k = q.shape
+    if k % W4_BLOCK_K:
+        raise ValueError(f'INT8 tiles need k % 128 == 0, got k={k}')
+    qp = np.zeros((_ceil16(n), k), dtype=np.int8)
+    qp[:n] = q
+    # [t, i, b, p, kb, j] -> [t, b, p, kb, i, j]: lane l = 16*kb + i
+    v = qp.reshape(-1, 16, k // 128, 2, 4, 16).transpose(0, 2, 3, 4, 1, 5)
+    return np.ascontiguousarray(v).reshape(-1, k // 128, 2, 64, 16)
+
+
+def w8_unpack(tiles: np.ndarray, n: int, k: int) -> np.ndarray:
+    t = np.asarray(tiles, dtype=np.int8).reshape(-1, k // 128, 2, 4, 16, 16)
+    q = t.transpose(0, 4, 1, 2, 3, 5).reshape(-1, k)
+    return np.ascontiguousarray(q[:n])
+

@@ -1,0 +1,128 @@
+"""INT8 tile layout on the GPU: wq_w8_repack / wq_w8_unpack against the numpy
+model, and every INT8 linear over tiles (W8A16 GEMV, skinny, GEMM, the
+decode-step fusions, W8A8) bit-identical to the same linear over the
+row-major weight, which the other INT8 tests check against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qdq, synth, tile_layout
+from ondeviceinfer_amd import _native
+from ondeviceinfer_amd.weight_quantization import backend as wq
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize('n,k', [(16, 128), (40, 384), (1000, 1024), (5120, 5120)])
+def test_w8_repack_is_the_tile_model_and_round_trips(gpu, n, k):
+    q = np.random.default_rng(n + k).integers(-127, 128, (n, k)).astype(np.int8)
+    tiles = _native.w8_repack(dev(q, gpu))
+    assert tiles.tiles.numel() == -(-n // 16) * (k // 128) * 2048
+    assert np.array_equal(host(tiles.tiles).view(np.int8), tile_layout.w8_repack(q).reshape(-1))
+    assert np.array_equal(host(_native.w8_unpack(tiles)), q)
+
+
+def test_w8_repack_rejects_k_off_the_block(gpu):
+    with pytest.raises(ValueError, match="k % 128"):
+        _native.w8_repack(torch.zeros(16, 200, dtype=torch.int8, device=gpu))
+
+
+@pytest.mark.parametrize('m', [1, 3, 4, 16, 40, 64, 65, 200])
+@pytest.mark.parametrize('n,k', [(40, 256), (1000, 1024), (5120, 5120), (5120, 17408)])
+def test_w8a16_tiled_equals_row_major(gpu, m, n, k):
+    """Decode GEMV (m <= 4, with its k-split on 17408 -> 5120), skinny
+    (5 <= m <= 64) and prefill GEMM (m > 64): the same bits from either
+    layout; the row-major result is within the bar of the oracle."""
+    _, q, s, x = synth.int8_case(n, k, m, seed=m + n + k)
+    qd, sd, xd = dev(q, gpu), dev(s, gpu), dev(x, gpu)
+    bias = dev((np.random.default_rng(m).standard_normal(n) * 0.1).astype(np.float16), gpu) if m == 3 else None
+    y_rm = _native.w8a16_linear(xd, qd, sd, bias=bias)
+    y_t = _native.w8a16_linear(xd, _native.w8_repack(qd), sd, bias=bias)
+    assert torch.equal(y_rm, y_t), f'tiled != row-major m={m} n={n} k={k}'
+    if n * k <= 1 << 22:
+        ref = qdq.linear_fp32(x, qdq.dequantize_linear_weight(q, s), None if bias is None else host(bias))
+        assert qdq.parity_ok(qdq.parity_metrics(host(y_t), ref))
+
+
+@pytest.mark.parametrize('mode', [0, 1, 2])
+def test_w8a16_decode_fused_tiled_equals_row_major(gpu, mode):
+    k, n = 5120, 7168
+    _, q, s, _ = synth.int8_case(n, k, 1, seed=70 + mode)
+    rng = np.random.default_rng(mode)
+    res = (rng.standard_normal(n) * 4).astype(np.float16)
+    kw = {}
+    if mode == 2:
+        xin = (rng.standard_normal(2 * k) * 2).astype(np.float16)
+    else:
+        xin = (rng.standard_normal(k) * 3).astype(np.float16)
+    if mode == 1:
+        nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float16)
+        parts = (xin.astype(np.float32) ** 2).reshape(-1, 16).sum(-1).astype(np.float32)
+        kw = {'norm_weight': dev(nw, gpu), 'sumsq_in': dev(parts, gpu)}
+    qd, sd = dev(q, gpu), dev(s, gpu)
+    outs = []
+    for w in (qd, _native.w8_repack(qd)):
+        hid = dev(res.copy(), gpu)
+        ss = torch.zeros(n // 16, dtype=torch.float32, device=gpu)
+        _native.w8a16_decode_fused(dev(xin, gpu), w, sd, x_mode=mode, residual=hid, sumsq_out=ss, out=hid, **kw)
+        outs.append((hid, ss))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize('m', [1, 8, 16, 17, 100, 256])
+@pytest.mark.parametrize('n,k', [(40, 256), (5120, 5120)])
+def test_w8a8_tiled_equals_row_major(gpu, m, n, k):
+    _, q, s, x = synth.int8_case(n, k, m, seed=90 + m)
+    qx, sx = _native.w8a8_quantize(dev(x, gpu))
+    qd = dev(q, gpu)
+    ws = dev(s.astype(np.float32), gpu)
+    y_rm = _native.w8a8_linear(qx, sx, qd, ws)
+    y_t = _native.w8a8_linear(qx, sx, _native.w8_repack(qd), ws)
+    assert torch.equal(y_rm, y_t), f'W8A8 tiled != row-major m={m} n={n} k={k}'
+
+
+def test_w8a16_tiled_k_beyond_gemm_offsets(gpu):
+    """k = 2^23 + 128 (past the prefill GEMM's largest k) at m = 66: the tiled
+    path runs the skinny kernel 64 rows at a time; sampled rows equal the
+    row-major any-shape kernel's within the bar and the oracle's."""
+    m, k, n = 66, (1 << 23) + 128, 16
+    rows = np.array([0, 1, 63, 64, 65])
+    _, q, s, _ = synth.int8_case(n, k, 1, seed=33)
+    x = torch.randn(m, k, device=gpu, dtype=torch.float16)
+    y = host(_native.w8a16_linear(x, _native.w8_repack(dev(q, gpu)), dev(s, gpu)))
+    xr = host(x[torch.from_numpy(rows).to(gpu)])
+    del x
+    ref = qdq.linear_fp32(xr, qdq.dequantize_linear_weight(q, s))
+    assert qdq.parity_ok(qdq.parity_metrics(y[rows], ref))
+
+
+def test_prepared_int8_fusion_keeps_tiles(gpu):
+    """The w8a16 backend prepares tiles; fusing q|k|v concatenates them and
+    the fused linear equals the parts' linears side by side, bit for bit."""
+    backend = wq.CompressedLinearBackend('w8a16')
+    layer, ref = {}, {}
+    for name, n in (('self_attn.q_proj', 256), ('self_attn.k_proj', 64), ('self_attn.v_proj', 64)):
+        _, q, s, _ = synth.int8_case(n, 512, 1, seed=n)
+        layer[name + '.weight'] = dev(q, gpu)
+        layer[name + '.weight_scale'] = dev(s.reshape(-1, 1), gpu)
+        backend.prepare(layer, name + '.weight')
+        assert isinstance(layer[name + '._prepared'].qweight, _native.W8Tiles)
+        ref[name] = layer[name + '.weight']
+    backend.fuse_projections(layer)
+    fused = layer['self_attn.qkv_proj._prepared']
+    assert isinstance(fused.qweight, _native.W8Tiles) and fused.n == 384
+    x = torch.randn(5, 512, device=gpu, dtype=torch.float16)
+    y = backend.linear(x, layer, 'self_attn.qkv_proj.weight')
+    parts = [backend.linear(x, layer, p + '.weight') for p in ('self_attn.q_proj', 'self_attn.k_proj',
+                                                              'self_attn.v_proj')]
+    assert torch.equal(y, torch.cat(parts, dim=1))
+    rm = torch.cat([_native.w8a16_linear(x, ref[p], layer[p + '._prepared'].scale) for p in ref], dim=1)
+    assert torch.equal(y, rm)

@@ -220,6 +220,29 @@ def test_w4_tile_round_trip_and_dequant(n, k, g, sym):
                           qdq.decode_weight(weights, 'p.weight', group_size=g).view(np.uint16))
 
 
+@pytest.mark.parametrize('n,k', [(16, 128), (40, 384), (1000, 256)])
+def test_w8_tile_layout_round_trip_and_lane_products(n, k):
+    """The INT8 tile model: unpack(repack(q)) == q, rows past n are zero, and
+    summing, per (tile, block, piece, lane), the lane's 16 bytes times x at
+    the k the INT8 kernels pair them with (128b + 64p + 16*(l//16) + j, row
+    16t + l%16) gives q @ x exactly: every weight meets its own x once."""
+    rng = np.random.default_rng(n + k)
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    x = rng.integers(-1000, 1000, k).astype(np.int64)
+    t = tile_layout.w8_repack(q)
+    assert t.shape == (-(-n // 16), k // 128, 2, 64, 16) and t.dtype == np.int8
+    assert np.array_equal(tile_layout.w8_unpack(t, n, k), q)
+    y = np.zeros(t.shape[0] * 16, dtype=np.int64)
+    j = np.arange(16)
+    for tt in range(t.shape[0]):
+        for b in range(k // 128):
+            for p in range(2):
+                for lane in range(64):
+                    y[16 * tt + lane % 16] += t[tt, b, p, lane].astype(np.int64) @ x[128 * b + 64 * p + 16 * (lane // 16) + j]
+    assert np.array_equal(y[:n], q.astype(np.int64) @ x)
+    assert not y[n:].any()
+
+
 def test_awq_synthetic_quantizer_is_valid_and_close():
     n, k = 32, 512
     rng = np.random.default_rng(0)
