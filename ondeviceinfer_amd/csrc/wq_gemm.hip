@@ -456,15 +456,16 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
 // slices of 32-row tiles on the deep ring (NT = 1, MT = 2, D = 6).  The
 // narrow shapes gain most (k_proj 5120->1024: M = 2048 46.7 -> 38.0 us,
 // M = 512 37.4 -> 21.8 us; down 17408->5120 at M = 128 101 -> 77 us; 5120^2
-// at M = 2048 155 -> 127 us).  The W8 weight loads (16 rows x 64 B) lose from
-// two tiles per wave: W8 keeps 64-wide slices of 64-row (M <= 256) or 128-row
-// tiles.
+// at M = 2048 155 -> 127 us).  INT8 tiles take the same grids (5120^2 at
+// M = 2048 190 -> 159 us, k_proj at M = 512 48 -> 22 us); row-major INT8,
+// whose weight loads are 16 rows x 64 B, loses from two tiles per wave and
+// keeps 64-wide slices of 64-row (M <= 256) or 128-row tiles.
 template <GFmt F>
 int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
                      const half_t* bias, half_t* y, hipStream_t s, int w8_tiled) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128;
   if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
-  if constexpr (F == GFmt::W4) {
+  if (F == GFmt::W4 || w8_tiled) {
     constexpr long kMinGrid = 384;
     const long mb64 = (M + 63) / 64;
     if (((ntile + 7) / 8) * mb64 >= kMinGrid)

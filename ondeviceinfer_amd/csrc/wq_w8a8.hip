@@ -290,10 +290,13 @@ int w8a8_linear_impl(const int8_t* qx, const float* x_scale, int64_t m, int64_t 
   if (m > kW8A8GemvMaxM && k % kI8Blk == 0) {
     // GEMM: 128-row x tiles for long batches, 32-row ones otherwise; four
     // weight tiles per wave while that still leaves a full machine of
-    // workgroups, else one.
+    // workgroups, else one.  Over INT8 tiles, long batches take two tiles
+    // per wave while that gives 512 workgroups (M = 4096: 5120^2 197 ->
+    // 159 us, 5120->17408 513 -> 454 us, 17408->5120 466 -> 410 us).
     const bool big_m = m >= 256;
     const int64_t mblocks = big_m ? (m + 127) / 128 : (m + 31) / 32;
-    const int nt = (ntile + 15) / 16 * mblocks >= 256 ? 4 : 1;
+    const bool two_tiles = tiled && big_m && (ntile + 7) / 8 * mblocks >= 512;
+    const int nt = two_tiles ? 2 : (ntile + 15) / 16 * mblocks >= 256 ? 4 : 1;
     WQ_REQUIRE(mblocks <= 65535, WQ_ERR_UNSUPPORTED, "too many rows for the W8A8 GEMM grid");
     const dim3 grid((unsigned)((ntile + 4 * nt - 1) / (4 * nt)), (unsigned)mblocks);
     auto launch = [&](auto kernel) {
@@ -301,7 +304,9 @@ int w8a8_linear_impl(const int8_t* qx, const float* x_scale, int64_t m, int64_t 
                          w_scale, b, (int)n, yy, wl8);
     };
     if (big_m) {
-      if (nt == 4) launch(w8a8_gemm_kernel<4, 8>); else launch(w8a8_gemm_kernel<1, 8>);
+      if (nt == 4) launch(w8a8_gemm_kernel<4, 8>);
+      else if (nt == 2) launch(w8a8_gemm_kernel<2, 8>);
+      else launch(w8a8_gemm_kernel<1, 8>);
     } else {
       if (nt == 4) launch(w8a8_gemm_kernel<4, 2>); else launch(w8a8_gemm_kernel<1, 2>);
     }

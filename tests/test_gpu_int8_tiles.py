@@ -52,6 +52,17 @@ def test_w8a16_tiled_equals_row_major(gpu, m, n, k):
         assert qdq.parity_ok(qdq.parity_metrics(host(y_t), ref))
 
 
+@pytest.mark.parametrize('m', [512, 1024, 2048])
+@pytest.mark.parametrize('n,k', [(1024, 5120), (5120, 5120)])
+def test_w8a16_tiled_prefill_grids_equal_row_major(gpu, m, n, k):
+    """Tiles take the W4 grid choice (two tiles per wave, 64-row tiles, the
+    deep ring on 32-row tiles), row-major INT8 its own; both sum every output
+    in the same order."""
+    _, q, s, x = synth.int8_case(n, k, m, seed=m + n)
+    qd, sd, xd = dev(q, gpu), dev(s, gpu), dev(x, gpu)
+    assert torch.equal(_native.w8a16_linear(xd, qd, sd), _native.w8a16_linear(xd, _native.w8_repack(qd), sd))
+
+
 @pytest.mark.parametrize('mode', [0, 1, 2])
 def test_w8a16_decode_fused_tiled_equals_row_major(gpu, mode):
     k, n = 5120, 7168
@@ -77,7 +88,7 @@ def test_w8a16_decode_fused_tiled_equals_row_major(gpu, mode):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
-@pytest.mark.parametrize('m', [1, 8, 16, 17, 100, 256])
+@pytest.mark.parametrize('m', [1, 8, 16, 17, 100, 256, 2048])
 @pytest.mark.parametrize('n,k', [(40, 256), (5120, 5120)])
 def test_w8a8_tiled_equals_row_major(gpu, m, n, k):
     _, q, s, x = synth.int8_case(n, k, m, seed=90 + m)
