@@ -388,10 +388,17 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
 template <int NCM>
 __global__ __launch_bounds__(128) void decode_attention_merge_kernel(int NC, const float* __restrict__ ws_o,
                                                                      const float2_t* __restrict__ ws_ml,
-                                                                     half_t* __restrict__ out) {
+                                                                     half_t* __restrict__ out, int xcd_group) {
   constexpr int D = kHeadDim;
   static_assert(NCM <= kMaxChunks && kMaxChunks <= 64, "one chunk per lane");
-  const int qh = blockIdx.x, d = threadIdx.x, lane = d & 63;
+  // With 8 kv heads the attention's workgroups of kv head h all run on XCD h
+  // (workgroups are dealt to the 8 XCDs round-robin by flat id h + 8c), so
+  // its partials sit in that XCD's L2; xcd_group = query heads per kv head
+  // then maps workgroup b to query head (b % 8) * xcd_group + b / 8, which
+  // lands on the same XCD.  0 = launch order.
+  const int b = blockIdx.x;
+  const int qh = xcd_group > 0 ? (b & 7) * xcd_group + (b >> 3) : b;
+  const int d = threadIdx.x, lane = d & 63;
   const float* po = ws_o + (size_t)qh * NC * D + d;
   float part[NCM];
 #pragma unroll
@@ -555,8 +562,9 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
                  : nc <= 32 ? decode_attention_merge_kernel<32>
                  : nc <= 48 ? decode_attention_merge_kernel<48>
                             : decode_attention_merge_kernel<64>;
+    const int xcd_group = kv_heads == 8 ? g : 0;   // 11.14 -> 11.03 us per layer with the merge (40 / 8 heads)
     hipLaunchKernelGGL(merge, dim3((unsigned)q_heads), dim3(kHeadDim), 0, as_stream(stream), (int)nc, po,
-                       reinterpret_cast<const float2_t*>(ml), reinterpret_cast<half_t*>(out));
+                       reinterpret_cast<const float2_t*>(ml), reinterpret_cast<half_t*>(out), xcd_group);
     return check_launch("decode_attention_merge");
   }
   return check_launch("decode_attention");
