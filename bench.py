@@ -31,10 +31,12 @@ Also in the same JSON line:
 * ``batch_sweep``: fused QKV, fused gate_up and a W4 lm_head at
   M in {1, 8, 32, 128, 512}, GB/s and TFLOP/s per launch;
 * ``int8``: configs[0]'s INT8 weight shape on the GPU over a pool of 40
-  distinct weights (1.05 GB, past the 256 MB Infinity Cache): weight-only
-  W8A16 and W8A8 (``int8_gemm``) decode GB/s, M=4096 W8A16 TFLOP/s and W8A8
-  TOPS against the fp16 / int8 MFMA peaks, and the vendor library's int8
-  GEMM (torch._int_mm) at M=4096 for context;
+  distinct weights (1.05 GB, past the 256 MB Infinity Cache), streamed as the
+  INT8 tiles the prepared linears use: weight-only W8A16 and W8A8
+  (``int8_gemm``) decode GB/s, M=4096 W8A16 TFLOP/s and W8A8 TOPS against the
+  fp16 / int8 MFMA peaks; the W8A16 pair once more over the row-major weight
+  as stored; the vendor library's int8 GEMM (torch._int_mm) at M=4096 for
+  context;
 * ``int8_e2e``: the INT8 weight-only model (INT8 v1 tensors, the reference's
   first published row) on the same workload, tok/s;
 * ``e2e_w4_lm_head``: the headline workload with the optional W4 LM head
