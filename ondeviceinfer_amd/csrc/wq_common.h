@@ -52,7 +52,9 @@ struct W8Layout {
   }
 };
 // Word 3 of a gfx9 buffer resource: 32-bit data format, so raw dword loads
-// are range-checked against num_records and return 0 past it.
+// are range-checked against num_records and return 0 past it.  On gfx950 the
+// check covers the SGPR offset (soffset) as well as the VGPR offset, so a
+// tile or row offset passed in soffset past the end also reads zero.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
 // Cache policy of a buffer access that is coherent across the XCDs' L2s
