@@ -81,6 +81,23 @@ int wq_prefill_qk_rope(const uint16_t* qkv, int64_t tokens, int64_t q_heads, int
                        const uint16_t* cos_rows, const uint16_t* sin_rows, int64_t start, uint16_t* key_cache,
                        uint16_t* value_cache, int64_t max_seq, uint16_t* q_out, void* stream);
 
+/* Prefill (tokens >= 1, batch 1) causal grouped-query attention over the
+ * resident cache, head_dim 128:
+ *   q            [tokens, q_heads, 128] fp16, token-major (wq_prefill_qk_rope's
+ *                q_out), query t at position start + t
+ *   key/value_cache [kv_heads, max_seq, 128] fp16; rows 0 .. start+tokens-1
+ *                hold the keys and values (this call's rows appended already)
+ *   out          [tokens, q_heads, 128] fp16, token-major
+ * Query t attends keys 0 .. start + t with weights softmax(scale * q.k),
+ * accumulated in fp32 with the probabilities rounded to fp16 for the value
+ * product (flash-attention order: the scores never reach memory).
+ * Replaces: F.scaled_dot_product_attention(is_causal / absolute causal mask,
+ * enable_gqa=True) over the cached keys in a multi-token forward
+ * (attention.py:35-85, quantized_model.py:186-199). */
+int wq_prefill_attention(const uint16_t* q, int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                         const uint16_t* key_cache, const uint16_t* value_cache, int64_t max_seq, int64_t start,
+                         float scale, uint16_t* out, void* stream);
+
 /* Workspace bytes for wq_lm_head with token != NULL (the per-wave argmax
  * candidates; no initialization needed). */
 int wq_lm_head_workspace_size(int64_t k, int64_t vocab, size_t* bytes);

@@ -75,6 +75,7 @@ _SIGNATURES = {
     'wq_decode_attention': [_P, _I64, _I64, _I64, _P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _I64,
                             ctypes.c_float, _P, _P, ctypes.c_size_t, _P],
     'wq_prefill_qk_rope': [_P, _I64, _I64, _I64, _I64, _P, _P, ctypes.c_float, _P, _P, _I64, _P, _P, _I64, _P, _P],
+    'wq_prefill_attention': [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, ctypes.c_float, _P, _P],
     'wq_lm_head_workspace_size': [_I64, _I64, _SIZE_P],
     'wq_argmax_f16_workspace_size': [_I64, _SIZE_P],
     'wq_argmax_f16': [_P, _I64, _P, _P, ctypes.c_size_t, _P],
@@ -641,6 +642,32 @@ def decode_attention(qkv: torch.Tensor, q_heads: int, kv_heads: int, q_norm: tor
     _call('wq_decode_attention', _ptr(qkv), q_heads, kv_heads, head_dim, _ptr(q_norm), _ptr(k_norm), float(eps),
           _ptr(cos_table), _ptr(sin_table), _ptr(position), _ptr(key_cache), _ptr(value_cache), max_seq,
           float(scale), _ptr(out), ws_ptr, ws_bytes, _stream(device))
+    return out
+
+
+def prefill_attention(query: torch.Tensor, q_heads: int, kv_heads: int, key_cache: torch.Tensor,
+                      value_cache: torch.Tensor, start: int, scale: float,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal GQA attention of ``tokens`` queries at positions ``start ..``
+    (batch 1) over cache rows ``0 .. start + tokens - 1``, which must already
+    hold these tokens' keys and values: ``query`` and the result are
+    token-major ``[tokens, q_heads, head_dim]`` fp16 (``wq_prefill_qk_rope``'s
+    q layout), the caches ``[kv_heads, max_seq, head_dim]``."""
+    device = _require_gpu(query, key_cache, value_cache, out)
+    if key_cache.dim() != 3 or key_cache.shape != value_cache.shape or key_cache.shape[0] != kv_heads:
+        raise ValueError(f'caches must be [kv_heads={kv_heads}, max_seq, head_dim], got {tuple(key_cache.shape)}')
+    _, max_seq, head_dim = key_cache.shape
+    for t, name in ((key_cache, 'key_cache'), (value_cache, 'value_cache')):
+        _check(t, torch.float16, (kv_heads, max_seq, head_dim), name)
+    if query.dim() != 3 or query.shape[1:] != (q_heads, head_dim):
+        raise ValueError(f'query must be [tokens, {q_heads}, {head_dim}], got {tuple(query.shape)}')
+    _check(query, torch.float16, tuple(query.shape), 'query')
+    if out is None:
+        out = torch.empty_like(query)
+    else:
+        _check(out, torch.float16, tuple(query.shape), 'out')
+    _call('wq_prefill_attention', _ptr(query), query.shape[0], q_heads, kv_heads, head_dim, _ptr(key_cache),
+          _ptr(value_cache), max_seq, start, float(scale), _ptr(out), _stream(device))
     return out
 
 
