@@ -96,7 +96,7 @@ import weakref  # noqa: E402
 
 import torch.nn.functional as F  # noqa: E402
 
-from .attention import cached_scaled_dot_product_attention, strided_prefill_attention  # noqa: E402
+from .attention import cached_scaled_dot_product_attention  # noqa: E402
 from .cache import KVCache, ResidentKVCache, kv_block  # noqa: E402
 from .functional import add_rms_norm, rms_norm  # noqa: E402
 from .layers import RotaryEmbedding, apply_rotary_pos_emb  # noqa: E402
@@ -127,7 +127,9 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     Same operation order and signature as the reference; when the backend
     prepared fused QKV / gate_up weights (``fuse_projections``) the three and
     the two projections run as one linear each, and ``silu(gate) * up`` runs
-    as one HIP kernel.
+    as one HIP kernel.  With a resident batch-1 cache the q/k norms, RoPE and
+    cache append run as one HIP kernel and the causal attention as another
+    (``wq_prefill_attention``, reading the cache rows in place).
     """
     def linear(inputs, name):
         if linear_backend is not None:
@@ -151,15 +153,17 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
         end = start + query_length
         if end > cache.max_seq_len:
             raise ValueError(f'KV cache capacity exceeded: requested {end}, capacity {cache.max_seq_len}')
-        # q comes back token-major [T, hq, d]; attention reads it and the cache
-        # rows in place and writes token-major output (no layout copies).
+        # q comes back token-major [T, hq, d]; the flash attention kernel reads
+        # it and the cache rows in place and writes token-major output (no
+        # layout copies).
         query = _native.prefill_qk_rope(
             qkv.view(query_length, -1), hq, hkv, weights['self_attn.q_norm.weight'],
             weights['self_attn.k_norm.weight'], eps, cos[0], sin[0], start, cache.key_cache[layer_idx][0],
-            cache.value_cache[layer_idx][0]).transpose(0, 1).unsqueeze(0)
+            cache.value_cache[layer_idx][0])
         cache.lengths[layer_idx] = end
-        attention_output = strided_prefill_attention(
-            query, cache.key_cache[layer_idx][:, :, :end], cache.value_cache[layer_idx][:, :, :end])
+        attention_output = _native.prefill_attention(
+            query, hq, hkv, cache.key_cache[layer_idx][0], cache.value_cache[layer_idx][0], start,
+            1.0 / float(d) ** 0.5).transpose(0, 1).unsqueeze(0)
     else:
         if qkv is not None:
             query, key, value = qkv.split((hq * d, hkv * d, hkv * d), dim=-1)
