@@ -86,7 +86,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
   const half_t* kbase = kc + (size_t)kvh * max_seq * kPD;
   const half_t* vbase = vc + (size_t)kvh * max_seq * kPD;
   // Block loads: K rows r = (tid + 256 u) / 16, 16-byte chunk (tid % 16);
-  // V key group 4 (tid / 16) .. +3, d chunk tid % 16.
+  // V keys 4 (tid % 16) .. +3, d chunk tid / 16 (so that the 16 lanes of a
+  // transposed V^T write cover one whole 128-byte row, not 16 rows).
   uint4_t kr[4], vr[4];
   auto load_block = [&](int kb) {
 #pragma unroll
@@ -97,31 +98,31 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int key = kb * kPBN + 4 * (tid >> 4) + e;
-      const int row = min(key, max_seq - 1);
-      const uint4_t v = *reinterpret_cast<const uint4_t*>(vbase + (size_t)row * kPD + 8 * (tid & 15));
-      vr[e] = key < key_end ? v : uint4_t{0u, 0u, 0u, 0u};
+      const int row = min(kb * kPBN + 4 * (tid & 15) + e, max_seq - 1);
+      vr[e] = *reinterpret_cast<const uint4_t*>(vbase + (size_t)row * kPD + 8 * (tid >> 4));
     }
   };
-  auto store_block = [&](int st) {
+  // The stores zero the values of keys past key_end (not in load_block, so
+  // that the loads stay in flight during the block's math).
+  auto store_block = [&](int st, int kb) {
     uint8_t* base = smem + st * kPStage;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int c = tid + 256 * u, r = c >> 4, cc = c & 15;
       *reinterpret_cast<uint4_t*>(base + r * 256 + ((cc ^ (r & 15)) << 4)) = kr[u];
     }
-    // Keys 4g .. 4g+3 (g = tid / 16) land in slots pos .. pos+3 of each of
+    // Keys 4g .. 4g+3 (g = tid % 16) land in slots pos .. pos+3 of each of
     // the chunk's 8 V^T rows.
-    const int g = tid >> 4, kk = (4 * g) & 31;
+    const int g = tid & 15, kk = (4 * g) & 31;
     const int pos = 32 * (g >> 3) + 8 * ((kk & 15) >> 2) + (kk >= 16 ? 4 : 0);
-    const int d0 = 8 * (tid & 15);
+    const int d0 = 8 * (tid >> 4);
 #pragma unroll
     for (int dd = 0; dd < 8; ++dd) {
       const int w = dd >> 1, hi = dd & 1;
       half4_t h4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t word = vr[e][w];
+        const uint32_t word = kb * kPBN + 4 * g + e < key_end ? vr[e][w] : 0u;
         h4[e] = __builtin_bit_cast(half2_t, word)[hi];
       }
       *reinterpret_cast<half4_t*>(base + vt_offset(d0 + dd, pos)) = h4;
@@ -136,7 +137,15 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
   float m_run[2] = {-INFINITY, -INFINITY};
 
   load_block(0);
-  store_block(0);
+  // Q and block 0 land here: the Q fragments must not be left in flight
+  // into the loop, where every iteration's wait would then also cover the
+  // next block's loads (the empty asm pins the Q loads above this point).
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(qf[qt][ks]));
+  __builtin_amdgcn_s_waitcnt(0);
+  store_block(0, 0);
   __syncthreads();
 
   float l_run[2] = {0.f, 0.f};   // this lane's part of each query's denominator
@@ -230,7 +239,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
       const uint8_t* base = smem + st * kPStage;
       step(base, k0, k0 + kPBN - 1 > wave_lo);
     }
-    if (more) store_block(st ^ 1);   // that stage was last read before the previous barrier
+    if (more) store_block(st ^ 1, kb + 1);   // that stage was last read before the previous barrier
     __syncthreads();
   }
 
