@@ -83,28 +83,31 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
     for (int ks = 0; ks < 4; ++ks) qf[qt][ks] = ld_h8(p + 32 * ks);
   }
 
-  const half_t* kbase = kc + (size_t)kvh * max_seq * kPD;
-  const half_t* vbase = vc + (size_t)kvh * max_seq * kPD;
+  // The kv head's cache rows as buffers (rows past max_seq read as zero).
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kc + (size_t)kvh * max_seq * kPD, (int64_t)max_seq * kPD * 2);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vc + (size_t)kvh * max_seq * kPD, (int64_t)max_seq * kPD * 2);
   // Block loads: K rows r = (tid + 256 u) / 16, 16-byte chunk (tid % 16);
   // V keys 4 (tid % 16) .. +3, d chunk tid / 16 (so that the 16 lanes of a
   // transposed V^T write cover one whole 128-byte row, not 16 rows).
   uint4_t kr[4], vr[4];
+  const uint32_t ko = (uint32_t)((tid >> 4) * 256 + (tid & 15) * 16);        // + 16 rows per u
+  const uint32_t vo = (uint32_t)(4 * (tid & 15) * 256 + (tid >> 4) * 16);   // + 1 row per e
   auto load_block = [&](int kb) {
+    const uint32_t so = (uint32_t)kb * kPBN * 256;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r = (tid + 256 * u) >> 4;
-      const int row = min(kb * kPBN + r, max_seq - 1);
-      kr[u] = *reinterpret_cast<const uint4_t*>(kbase + (size_t)row * kPD + 8 * (tid & 15));
-    }
+    for (int u = 0; u < 4; ++u) kr[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 4096 * u, so, 0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = min(kb * kPBN + 4 * (tid & 15) + e, max_seq - 1);
-      vr[e] = *reinterpret_cast<const uint4_t*>(vbase + (size_t)row * kPD + 8 * (tid >> 4));
-    }
+    for (int e = 0; e < 4; ++e) vr[e] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo + 256 * e, so, 0);
   };
   // The stores zero the values of keys past key_end (not in load_block, so
-  // that the loads stay in flight during the block's math).
+  // that the loads stay in flight during the block's math; only the last
+  // block has such keys).
   auto store_block = [&](int st, int kb) {
+    if (kb * kPBN + kPBN > key_end) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (kb * kPBN + 4 * (tid & 15) + e >= key_end) vr[e] = uint4_t{0u, 0u, 0u, 0u};
+    }
     uint8_t* base = smem + st * kPStage;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -122,7 +125,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
       half4_t h4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t word = kb * kPBN + 4 * g + e < key_end ? vr[e][w] : 0u;
+        // Through a scalar: a bit_cast of an ext-vector component reads
+        // component 0 in this hipcc.
+        const uint32_t word = vr[e][w];
         h4[e] = __builtin_bit_cast(half2_t, word)[hi];
       }
       *reinterpret_cast<half4_t*>(base + vt_offset(d0 + dd, pos)) = h4;
