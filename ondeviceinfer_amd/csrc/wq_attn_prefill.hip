@@ -3,21 +3,23 @@
 // query block's keys once through LDS and keeps the softmax online, so the
 // [tokens x keys] score matrix never exists in memory.
 //
-// Layout and arithmetic (head_dim 128, 16x16x32 fp16 MFMA, fp32 accumulate):
+// Layout and arithmetic (head_dim 128, 32x32x16 fp16 MFMA, fp32 accumulate):
 //  * workgroup = 4 waves = 128 queries of one query head; wave w owns the 32
-//    queries 32w .. 32w + 31 of the block (two 16-query tiles);
+//    queries 32w .. 32w + 31 of the block (one 32-query tile);
 //  * per 64-key block the keys go to LDS as K [key][d] (16-byte chunk c of
 //    row r at slot c ^ (r & 15)) and the values transposed as V^T [d][key
 //    slot] (chunk c of row d at slot c ^ ((d >> 1) & 7)), so the 16 lanes of
 //    a fragment read hit distinct banks;
-//  * scores are computed transposed, S^T = K . Q^T (A = 16 keys x 32 d from
-//    LDS, B = 32 d x 16 queries held in registers), so lane l holds keys
-//    4(l/16) .. 4(l/16)+3 of each 16-key tile for query l % 16;
+//  * scores are computed transposed, S^T = K . Q^T (A = 32 keys x 16 d from
+//    LDS, B = 16 d x 32 queries held in registers): lane l = (q, h) =
+//    (l % 32, l / 32) holds, in register r, key 8(r/4) + 4h + r%4 of each
+//    32-key tile for query q;
 //  * P^T, rounded to fp16, is then directly the B operand of O^T = V^T . P^T
-//    once V^T's key slots follow the same order: slot 8s + j holds key 4s + j
-//    and slot 8s + 4 + j key 16 + 4s + j of each 32-key step;
+//    (registers 8s .. 8s+7 for 16-key step s of a tile) once V^T's key slots
+//    follow the same order: slot 8h + 4j + e of a 16-key step holds key
+//    8j + 4h + e;
 //  * the online softmax runs in log2 units (scale * log2 e folded into the
-//    scores); a query's max is reduced over its four lanes with lane swaps;
+//    scores); a query's max is reduced over its two lanes with one lane swap;
 //    the denominator sums the fp32 P per lane and is reduced once at the end;
 //    the accumulators are rescaled only in blocks where some query's maximum
 //    moved.
@@ -37,6 +39,8 @@ constexpr int kPBN = 64;                    // keys per block
 constexpr int kPKBytes = kPBN * kPD * 2;    // K block in LDS
 constexpr int kPVBytes = kPD * kPBN * 2;    // V^T block in LDS
 constexpr int kPStage = kPKBytes + kPVBytes;
+
+typedef float float16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __builtin_bit_cast(float, __shfl_xor(__builtin_bit_cast(int, v), mask, 64));
@@ -59,7 +63,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int i = lane & 15, s4 = lane >> 4;
+  const int ql = lane & 31, hh = lane >> 5;   // this lane's query within the wave's tile, and lane half
   const int G = H / KV;
   const int b = blockIdx.x;
   const int kvh = b % KV, j = b / KV;
@@ -71,16 +75,16 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
   const int nkb = (key_end + kPBN - 1) / kPBN;
   const int wave_lo = start + q0;                                 // this wave's first query position
   const int wave_hi = start + min(q0 + 31, T - 1);                // ... and last (q0 < T or the wave is idle)
+  const int qpos = start + q0 + ql;                               // this lane's query position
 
-  // Q^T fragments (B operand): query q0 + 16qt + i (clamped; rows past T are
-  // computed, never stored), d = 32ks + 8 s4 .. +7.
-  half8_t qf[2][4];
+  // Q^T fragments (B operand): query q0 + ql (clamped; rows past T are
+  // computed, never stored), d = 16ks + 8hh .. +7.
+  half8_t qf[8];
+  {
+    const int t = min(q0 + ql, T - 1);
+    const half_t* p = q + ((size_t)t * H + qh) * kPD + 8 * hh;
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int t = min(q0 + 16 * qt + i, T - 1);
-    const half_t* p = q + ((size_t)t * H + qh) * kPD + 8 * s4;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[qt][ks] = ld_h8(p + 32 * ks);
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = ld_h8(p + 16 * ks);
   }
 
   // The kv head's cache rows as buffers (rows past max_seq read as zero).
@@ -115,9 +119,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
       *reinterpret_cast<uint4_t*>(base + r * 256 + ((cc ^ (r & 15)) << 4)) = kr[u];
     }
     // Keys 4g .. 4g+3 (g = tid % 16) land in slots pos .. pos+3 of each of
-    // the chunk's 8 V^T rows.
-    const int g = tid & 15, kk = (4 * g) & 31;
-    const int pos = 32 * (g >> 3) + 8 * ((kk & 15) >> 2) + (kk >= 16 ? 4 : 0);
+    // the chunk's 8 V^T rows: within 16-key step g / 4, key 8jj + 4h + e
+    // sits at slot 8h + 4jj + e.
+    const int g = tid & 15, kk = (4 * g) & 15;
+    const int pos = 16 * (g >> 2) + 8 * ((kk & 7) >> 2) + 4 * (kk >> 3);
     const int d0 = 8 * (tid >> 4);
 #pragma unroll
     for (int dd = 0; dd < 8; ++dd) {
@@ -134,104 +139,95 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
     }
   };
 
-  float4_t acc[8][2];
+  float16_t acc[4];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) acc[dt][qt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY};
+    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;   // this lane's part of its query's denominator
 
   load_block(0);
   // Q and block 0 land here: the Q fragments must not be left in flight
   // into the loop, where every iteration's wait would then also cover the
   // next block's loads (the empty asm pins the Q loads above this point).
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(qf[qt][ks]));
+  for (int ks = 0; ks < 8; ++ks) asm volatile("" : "+v"(qf[ks]));
   __builtin_amdgcn_s_waitcnt(0);
   store_block(0, 0);
   __syncthreads();
 
-  float l_run[2] = {0.f, 0.f};   // this lane's part of each query's denominator
-
   // One 64-key block of this wave's 32 queries; `masked`: some keys of the
   // block lie past some of the wave's query positions (wave-uniform).
   auto step = [&](const uint8_t* base, int k0, bool masked) {
-    // S^T = K . Q^T for the block's four 16-key tiles.
-    float4_t sc[4][2];
+    // S^T = K . Q^T for the block's two 32-key tiles.
+    float16_t sc[2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      sc[kt][0] = sc[kt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
-      const int r = 16 * kt + i;
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int cc = 4 * ks + s4;
-        const half8_t a = *reinterpret_cast<const half8_t*>(base + r * 256 + ((cc ^ (r & 15)) << 4));
-        sc[kt][0] = mfma16(a, qf[0][ks], sc[kt][0]);
-        sc[kt][1] = mfma16(a, qf[1][ks], sc[kt][1]);
+      for (int r = 0; r < 16; ++r) sc[kt][r] = 0.f;
+      const int row = 32 * kt + ql;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int cc = 2 * ks + hh;
+        const half8_t a = *reinterpret_cast<const half8_t*>(base + row * 256 + ((cc ^ (row & 15)) << 4));
+        sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], sc[kt], 0, 0, 0);
       }
     }
     if (masked) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (k0 + 16 * kt + 4 * s4 + v > start + q0 + 16 * qt + i) sc[kt][qt][v] = -INFINITY;
+        for (int r = 0; r < 16; ++r)
+          if (k0 + 32 * kt + 8 * (r >> 2) + 4 * hh + (r & 3) > qpos) sc[kt][r] = -INFINITY;
     }
+    float mb = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mb = fmaxf(mb, sc[kt][r]);
+    mb = fmaxf(mb, shfl_xor_f(mb, 32));
+    // scale_log2 > 0, so the scaled maximum is the maximum of the scaled scores.
+    const float m_new = fmaxf(m_run, mb * scale_log2);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2_hw(m_run - m_use);   // 0 on the first block with a key
+    m_run = m_new;
     half8_t pb[2][2];
-    float alpha[2];
+    float ls = 0.f;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float mb = -INFINITY;
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int st = 0; st < 2; ++st) {
+        half8_t h;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) mb = fmaxf(mb, sc[kt][qt][v]);
-      mb = fmaxf(mb, shfl_xor_f(mb, 16));
-      mb = fmaxf(mb, shfl_xor_f(mb, 32));
-      // scale_log2 > 0, so the scaled maximum is the maximum of the scaled scores.
-      const float m_new = fmaxf(m_run[qt], mb * scale_log2);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      alpha[qt] = exp2_hw(m_run[qt] - m_use);   // 0 on the first block with a key
-      m_run[qt] = m_new;
-      half_t ph[4][4];
-      float ls = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float p = exp2_hw(__builtin_fmaf(sc[kt][qt][v], scale_log2, -m_use));
-          ls += p;
-          ph[kt][v] = (half_t)p;
+        for (int e = 0; e < 8; ++e) {
+          const float pv = exp2_hw(__builtin_fmaf(sc[kt][8 * st + e], scale_log2, -m_use));
+          ls += pv;
+          h[e] = (half_t)pv;
         }
-      l_run[qt] = l_run[qt] * alpha[qt] + ls;
-#pragma unroll
-      for (int kv = 0; kv < 2; ++kv)
-        pb[qt][kv] = half8_t{ph[2 * kv][0], ph[2 * kv][1], ph[2 * kv][2], ph[2 * kv][3],
-                             ph[2 * kv + 1][0], ph[2 * kv + 1][1], ph[2 * kv + 1][2], ph[2 * kv + 1][3]};
-    }
-    // Rescale only when some query's maximum moved (wave-uniform test).
-    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[dt][qt] *= alpha[qt];
-    }
-    // O^T += V^T . P^T
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int d = 16 * dt + i;
-#pragma unroll
-      for (int kv = 0; kv < 2; ++kv) {
-        const int ch = 4 * kv + s4;
-        const half8_t a =
-            *reinterpret_cast<const half8_t*>(base + kPKBytes + d * (kPBN * 2) + ((ch ^ ((d >> 1) & 7)) << 4));
-        acc[dt][0] = mfma16(a, pb[0][kv], acc[dt][0]);
-        acc[dt][1] = mfma16(a, pb[1][kv], acc[dt][1]);
+        pb[kt][st] = h;
       }
+    l_run = l_run * alpha + ls;
+    // Rescale only when some query's maximum moved (wave-uniform test).
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+    }
+    // O^T += V^T . P^T over the block's four 16-key steps.
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int d = 32 * dt + ql;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const int ch = 2 * (2 * kt + st) + hh;
+          const half8_t a =
+              *reinterpret_cast<const half8_t*>(base + kPKBytes + d * (kPBN * 2) + ((ch ^ ((d >> 1) & 7)) << 4));
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kt][st], acc[dt], 0, 0, 0);
+        }
     }
   };
 
@@ -240,32 +236,26 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const half_t*
     const bool more = kb + 1 < nkb;
     if (more) load_block(kb + 1);
     const int k0 = kb * kPBN;
-    if (q0 < T && k0 <= wave_hi) {
-      const uint8_t* base = smem + st * kPStage;
-      step(base, k0, k0 + kPBN - 1 > wave_lo);
-    }
+    if (q0 < T && k0 <= wave_hi) step(smem + st * kPStage, k0, k0 + kPBN - 1 > wave_lo);
     if (more) store_block(st ^ 1, kb + 1);   // that stage was last read before the previous barrier
     __syncthreads();
   }
 
-  // out[t][qh][d] = O / l; lane (i, s4) holds d = 16 dt + 4 s4 .. +3 of query 16 qt + i.
+  // out[t][qh][d] = O / l; lane (ql, hh) holds d = 32 dt + 8 (r/4) + 4 hh + r%4 of query ql.
+  const float l = l_run + shfl_xor_f(l_run, 32);
+  const float inv = 1.0f / l;
+  const int t = q0 + ql;
+  if (t < T) {
+    half_t* o = out + ((size_t)t * H + qh) * kPD + 4 * hh;
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    float l = l_run[qt];
-    l += shfl_xor_f(l, 16);
-    l += shfl_xor_f(l, 32);
-    const float inv = 1.0f / l;
-    const int t = q0 + 16 * qt + i;
-    if (t < T) {
-      half_t* o = out + ((size_t)t * H + qh) * kPD + 4 * s4;
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        half4_t h;
+      for (int jj = 0; jj < 4; ++jj) {
+        half4_t hv;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) h[v] = (half_t)(acc[dt][qt][v] * inv);
-        *reinterpret_cast<half4_t*>(o + 16 * dt) = h;
+        for (int e = 0; e < 4; ++e) hv[e] = (half_t)(acc[dt][4 * jj + e] * inv);
+        *reinterpret_cast<half4_t*>(o + 32 * dt + 8 * jj) = hv;
       }
-    }
   }
 }
 
