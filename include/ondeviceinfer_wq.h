@@ -150,6 +150,27 @@ int wq_w4a16_decode_fused(const uint16_t* x, int64_t k, const void* tiles, const
                           int64_t sumsq_count, float eps, const uint16_t* residual, float* sumsq_out, uint16_t* y,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Whether wq_w4a16_linear_epilogue applies to this shape and mode (1) or not
+ * (0): m above the decode GEMV's 64 rows, on the prefill GEMM grids that carry
+ * a fused epilogue (mode 1 also needs two tiles per wave and n % 32 == 0). */
+int wq_w4a16_epilogue_supported(int64_t m, int64_t n, int64_t k, int64_t group_size, int32_t mode);
+
+/* Prefill (m > 64) W4A16 linear with the next elementwise op of the Qwen3 MLP
+ * in its epilogue, bit-identical to wq_w4a16_linear followed by that op:
+ *   mode 1  W is a fused [gate | up] of n = 2 n_out rows (gate rows first);
+ *           y fp16 [m, n_out] = fp16(fp16(silu(g)) * u) with g, u the fp16
+ *           outputs of the gate and up rows (wq_silu_mul's arithmetic);
+ *   mode 2  y fp16 [m, n] = fp16(residual + fp16(x . W^T)); y may alias
+ *           residual.
+ * Shapes for which wq_w4a16_epilogue_supported is 0 return WQ_ERR_UNSUPPORTED.
+ * Replaces `F.silu(gate) * up` after the gate/up linears and
+ * `residual + mlp_output` after the down linear of the prefill forward
+ * (quantized_model.py:216-228), which the reference runs as separate torch
+ * ops after the linears. */
+int wq_w4a16_linear_epilogue(const uint16_t* x, int64_t m, int64_t k, const void* tiles, const void* meta,
+                             int64_t n, int64_t group_size, int32_t mode, const uint16_t* residual,
+                             uint16_t* y, void* stream);
+
 /* ------------------------------------------------- W8 (int8, per-output-channel scale) */
 
 /* fp16 [n, k] = fp16(q * scale[n]), scale fp32 [n].  Replaces the INT8 branch

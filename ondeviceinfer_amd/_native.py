@@ -51,6 +51,8 @@ _SIGNATURES = {
     'wq_w4a16_workspace_size': [_I64, _I64, _I64, _I64, _SIZE_P],
     'wq_w4a16_linear': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, ctypes.c_size_t, _P],
     'wq_w4a16_linear_noalloc': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P],
+    'wq_w4a16_epilogue_supported': [_I64, _I64, _I64, _I64, ctypes.c_int32],
+    'wq_w4a16_linear_epilogue': [_P, _I64, _I64, _P, _P, _I64, _I64, ctypes.c_int32, _P, _P, _P],
     'wq_w4a16_decode_fused': [_P, _I64, _P, _P, _I64, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P,
                               _P, _P, ctypes.c_size_t, _P],
     'wq_w8a16_decode_fused': [_P, _I64, _P, _P, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P, _P, _P,
@@ -324,6 +326,52 @@ def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: in
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     _call('wq_w4a16_linear', _ptr(x), m, k, _ptr(tiles), _ptr(meta), n, group_size, _ptr(out), ws_ptr, ws_bytes,
           _stream(device))
+    return out
+
+
+EPI_SILU_MUL, EPI_RESIDUAL = 1, 2
+
+
+def w4a16_epilogue_supported(m: int, n: int, k: int, group_size: int, mode: int) -> bool:
+    """Whether ``w4a16_linear_epilogue`` runs this shape (the prefill GEMM
+    grids that carry a fused epilogue; m > 64)."""
+    return bool(load().wq_w4a16_epilogue_supported(m, n, k, group_size, mode))
+
+
+def w4a16_linear_epilogue(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: int, group_size: int,
+                          mode: int, residual: torch.Tensor | None = None,
+                          out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill W4A16 linear with the MLP's next elementwise op fused in, bit-
+    identical to ``w4a16_linear`` followed by it.  ``EPI_SILU_MUL``: ``W`` is
+    a fused ``[gate | up]`` of ``n`` rows and the result is
+    ``silu(gate) * up`` as ``[m, n // 2]`` (``silu_mul``'s arithmetic).
+    ``EPI_RESIDUAL``: ``residual + x . W^T`` as ``[m, n]`` (``out`` may be
+    ``residual``).  Raises ``ValueError`` for shapes that
+    ``w4a16_epilogue_supported`` rejects."""
+    device = _require_gpu(x, tiles, meta, residual, out)
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise TypeError(f'x must be a 2-D float16 tensor, got {x.dtype} {tuple(x.shape)}')
+    if mode not in (EPI_SILU_MUL, EPI_RESIDUAL):
+        raise ValueError(f'mode must be EPI_SILU_MUL or EPI_RESIDUAL, got {mode}')
+    m, k = x.shape
+    n_out = n // 2 if mode == EPI_SILU_MUL else n
+    x = _aligned(x.contiguous())
+    res_ptr = None
+    if mode == EPI_RESIDUAL:
+        if residual is None:
+            raise ValueError('EPI_RESIDUAL needs a residual tensor')
+        _check(residual, torch.float16, (m, n), 'residual')
+        if not residual.is_contiguous() or residual.data_ptr() % 8:
+            raise ValueError('residual must be contiguous and 8-byte aligned')
+        res_ptr = residual.data_ptr()
+    if out is None:
+        out = torch.empty((m, n_out), dtype=torch.float16, device=device)
+    else:
+        _check(out, torch.float16, (m, n_out), 'out')
+        if not out.is_contiguous() or out.data_ptr() % 16:
+            raise ValueError('out must be contiguous and 16-byte aligned')
+    _call('wq_w4a16_linear_epilogue', _ptr(x), m, k, _ptr(tiles), _ptr(meta), n, group_size, mode, res_ptr,
+          _ptr(out), _stream(device))
     return out
 
 

@@ -323,9 +323,16 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // silu(g) = g / (1 + e^-g) as g * rcp(1 + 2^(-g log2 e)): two transcendental
 // ops instead of expf and an IEEE divide.  The fp32 result is within a few
 // ulp of the exact quotient, far below the fp16 rounding that follows it;
-// g -> -inf gives -0 (rcp(inf) = 0), g -> +inf gives g.
+// g -> -inf gives -0 (rcp(inf) = 0), g -> +inf gives g, silu(-0) = -0.
+// The empty asm keeps g and the product as plain fp32 values: otherwise
+// hipcc folds the fp16 -> fp32 widening of g, or the fp16 rounding of the
+// result, into a mixed-precision FMA with a +0 addend, which returns +0 for
+// g = -0 (and then a product with a negative up value differs in sign).
 __device__ __forceinline__ float silu_f(float g) {
-  return g * __builtin_amdgcn_rcpf(1.0f + exp2_hw(-g * kLog2e));
+  asm("" : "+v"(g));
+  float r = g * __builtin_amdgcn_rcpf(1.0f + exp2_hw(-g * kLog2e));
+  asm("" : "+v"(r));
+  return r;
 }
 
 }  // namespace wq

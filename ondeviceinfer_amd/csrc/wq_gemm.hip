@@ -21,7 +21,9 @@
 // The tile shape follows the grid size (launch_gemm_auto); grids whose
 // blocks are too short to hide a load run a deep-ring form with several
 // blocks in flight (wq_gemm_deep_kernel), with the same block math; from
-// M = 4096 on, W4 row blocks are assigned to XCDs (gemm_coords).
+// M = 4096 on, W4 row blocks are assigned to XCDs (gemm_coords).  The W4
+// kernel can also finish the Qwen3 MLP's elementwise ops in its epilogue
+// (Epi: silu(gate) * up over a fused [gate | up] weight, or a residual add).
 #include "wq_common.h"
 #include "wq_status.h"
 
@@ -31,6 +33,14 @@ namespace {
 constexpr int kRowBytes = kW4BlockK * 2;   // one activation row of a 128-k block
 
 enum class GFmt { W4, W8 };
+
+// Epilogue of the prefill GEMM.  SiluPair: the weight is a fused [gate | up]
+// of 2 * nh tiles and each wave's NT tiles are NT/2 gate tiles and the NT/2
+// up tiles of the same columns, so the wave writes fp16(fp16(silu(g)) * u)
+// (g, u the fp16-rounded sums) to an [M, N/2] output.  Residual:
+// y = fp16(residual + fp16(sum)).  Both equal the separate elementwise
+// kernel after a plain GEMM bit for bit.
+enum class Epi { Plain, SiluPair, Residual };
 
 template <GFmt F, int NT>
 struct WRegs;
@@ -146,6 +156,39 @@ __device__ __forceinline__ void gemm_store(const float4_t (&acc)[NT][MT], int ti
   }
 }
 
+// Epilogue of the fused modes (W4): lane holds D[n = 4*kb + v][m = i] as above.
+template <Epi EP, int NT, int MT>
+__device__ __forceinline__ void gemm_store_epi(const float4_t (&acc)[NT][MT], int tile0, int ntile, int m0, int M,
+                                               int N, int i, int kb, const half_t* __restrict__ res,
+                                               half_t* __restrict__ y) {
+  constexpr int NO = EP == Epi::SiluPair ? NT / 2 : NT;   // output tiles per wave
+  const int nout = EP == Epi::SiluPair ? N / 2 : N;
+  const int nt_out = EP == Epi::SiluPair ? ntile / 2 : ntile;
+#pragma unroll
+  for (int t = 0; t < NO; ++t) {
+    const int n0 = (tile0 + t) * 16 + 4 * kb;
+    if (tile0 + t >= nt_out || n0 >= nout) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 16 + i;
+      if (m >= M) continue;
+      half4_t o;
+      if constexpr (EP == Epi::SiluPair) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const half_t g = (half_t)acc[t][mt][v], u = (half_t)acc[t + NO][mt][v];
+          o[v] = (half_t)silu_f((float)g) * u;
+        }
+      } else {
+        const half4_t r = *reinterpret_cast<const half4_t*>(res + (size_t)m * N + n0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = (half_t)((float)(half_t)acc[t][mt][v] + (float)r[v]);
+      }
+      *reinterpret_cast<half4_t*>(y + (size_t)m * nout + n0) = o;
+    }
+  }
+}
+
 // Workgroup -> (n slice bx, row block by).  Workgroups go to the 8 XCDs
 // round-robin by flat id.  With rpx > 0 (the host sets it when the row blocks
 // divide by 8: rpx = row blocks / 8), XCD x takes row blocks
@@ -164,12 +207,14 @@ __device__ __forceinline__ void gemm_coords(int rpx, int& bx, int& by) {
   }
 }
 
-template <GFmt F, int NT, int MT>
+template <GFmt F, int NT, int MT, Epi EP = Epi::Plain>
 __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restrict__ x, int M, int K,
                                                          const void* __restrict__ wsrc,
                                                          const void* __restrict__ wmeta, int N, int bpg,
                                                          const half_t* __restrict__ bias, half_t* __restrict__ y, int rpx,
-                                                         int w8_tiled) {
+                                                         int w8_tiled, const half_t* __restrict__ res) {
+  static_assert(EP == Epi::Plain || F == GFmt::W4, "fused epilogues are W4 only");
+  static_assert(EP != Epi::SiluPair || NT % 2 == 0, "SiluPair pairs gate and up tiles");
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kRowBytes;
   constexpr int kInstrPerWave = BM * 16 / 64 / 4;   // 1 KiB direct loads per wave per stage
@@ -183,7 +228,11 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
   int bx, by;
   gemm_coords(rpx, bx, by);
   const int m0 = by * BM;
-  const int tile0 = (bx * 4 + wave) * NT;
+  // First tile of this wave (SiluPair: its first gate tile; the up tiles of
+  // the same columns sit nh tiles further on).
+  const int tile0 = (bx * 4 + wave) * (EP == Epi::SiluPair ? NT / 2 : NT);
+  const int nh = ntile / 2;
+  auto toff = [&](int t) { return EP == Epi::SiluPair && t >= NT / 2 ? nh + t - NT / 2 : t; };
 
   // Activation copy for block `blk` into stage `st`: instruction J of the
   // workgroup fills rows 4J..4J+3; lane L lands in row 4J + L/16, slot L%16,
@@ -228,9 +277,9 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
       const int ngrp = nblk / bpg, g = blk / bpg;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        r.w[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)lane * 16, (uint32_t)((t * nblk + blk) * 1024),
-                                                       kNtPolicy);
-        const uint32_t mo = (uint32_t)((t * ngrp + g) * kW4MetaBytes);
+        r.w[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)lane * 16,
+                                                       (uint32_t)((toff(t) * nblk + blk) * 1024), kNtPolicy);
+        const uint32_t mo = (uint32_t)((toff(t) * ngrp + g) * kW4MetaBytes);
         r.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rm, (uint32_t)i * 2, mo, 0);
         r.z[t] = __builtin_amdgcn_raw_buffer_load_b32(rm, 32 + (uint32_t)(i >> 3) * 4, mo, 0);
       }
@@ -274,7 +323,10 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
     __syncthreads();                  // ... and everyone's; stage st may be overwritten next
   }
 
-  gemm_store<F, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, wmeta, bias, y);
+  if constexpr (EP == Epi::Plain)
+    gemm_store<F, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, wmeta, bias, y);
+  else
+    gemm_store_epi<EP, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, res, y);
 }
 
 // Deep-ring form, for grids whose per-block math is short (wide N at
@@ -429,13 +481,15 @@ int xcd_rows(int M, unsigned grid_y) {
   return F == GFmt::W4 && M >= 4096 && grid_y % 8 == 0 ? (int)grid_y / 8 : 0;
 }
 
-template <GFmt F, int NT, int MT>
+template <GFmt F, int NT, int MT, Epi EP = Epi::Plain>
 int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
-                const half_t* bias, half_t* y, hipStream_t s, int w8_tiled) {
+                const half_t* bias, half_t* y, hipStream_t s, int w8_tiled, const half_t* res = nullptr) {
+  // SiluPair: N counts gate and up columns; a wave covers NT/2 of each, so
+  // the grid has the same number of n slices.
   const int ntile = (N + 15) / 16;
   const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)));
-  hipLaunchKernelGGL((wq_gemm_kernel<F, NT, MT>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y,
-                     xcd_rows<F>(M, grid.y), w8_tiled);
+  hipLaunchKernelGGL((wq_gemm_kernel<F, NT, MT, EP>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y,
+                     xcd_rows<F>(M, grid.y), w8_tiled, res);
   return check_launch(F == GFmt::W4 ? "w4_gemm" : "w8_gemm");
 }
 
@@ -484,6 +538,39 @@ int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* m
 int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
                    hipStream_t s) {
   return launch_gemm_auto<GFmt::W4>(x, M, K, tiles, meta, N, G / kW4BlockK, nullptr, y, s, 0);
+}
+
+// The grid launch_gemm_auto picks for a W4 shape, when it is a wq_gemm_kernel
+// grid that can carry a fused epilogue: 1 = NT 4 / MT 8, 2 = NT 2 / MT 4,
+// 3 = NT 1 / MT 4 (Residual only: SiluPair pairs tiles within a wave); 0
+// otherwise.  SiluPair also needs the up tiles' offsets (nh + NT tiles from
+// a wave's first tile) inside the 31-bit buffer range.
+int w4_gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode) {
+  const long ntile = (N + 15) / 16, mblk = (M + 127) / 128, mb64 = (M + 63) / 64;
+  int plan = 0;
+  if (((ntile + 15) / 16) * mblk >= 512) plan = 1;
+  else if (((ntile + 7) / 8) * mb64 >= 384) plan = 2;
+  else if (((ntile + 3) / 4) * mb64 >= 384) plan = 3;
+  if (mode == 1) {
+    if (plan == 3 || N % 32 != 0) return 0;
+    if ((ntile / 2 + 4) * (K / kW4BlockK) * 1024 > 0x7fffffffL) return 0;
+  }
+  return plan;
+}
+
+// W4 prefill GEMM with a fused epilogue (mode 1 SiluPair, 2 Residual); the
+// caller has checked w4_gemm_epi_plan.
+int launch_w4_gemm_epi(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
+                       int mode, const half_t* res, half_t* y, hipStream_t s) {
+  const int bpg = G / kW4BlockK;
+  switch (w4_gemm_epi_plan(M, N, K, mode) * 2 + (mode == 1 ? 0 : 1)) {
+    case 2: return launch_gemm<GFmt::W4, 4, 8, Epi::SiluPair>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
+    case 3: return launch_gemm<GFmt::W4, 4, 8, Epi::Residual>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0, res);
+    case 4: return launch_gemm<GFmt::W4, 2, 4, Epi::SiluPair>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
+    case 5: return launch_gemm<GFmt::W4, 2, 4, Epi::Residual>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0, res);
+    case 7: return launch_gemm<GFmt::W4, 1, 4, Epi::Residual>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0, res);
+    default: return fail(WQ_ERR_UNSUPPORTED, "w4 GEMM epilogue: shape has no fused-epilogue grid");
+  }
 }
 
 // Wide N at 16 < M <= 64: the deep ring keeps five weight blocks per wave in

@@ -127,7 +127,8 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     Same operation order and signature as the reference; when the backend
     prepared fused QKV / gate_up weights (``fuse_projections``) the three and
     the two projections run as one linear each, and ``silu(gate) * up`` runs
-    as one HIP kernel.  With a resident batch-1 cache the q/k norms, RoPE and
+    as one HIP kernel; on the prefill GEMM it and the MLP's residual add run
+    in the gate_up and down GEMMs' epilogues.  With a resident batch-1 cache the q/k norms, RoPE and
     cache append run as one HIP kernel and the causal attention as another
     (``wq_prefill_attention``, reading the cache rows in place).
     """
@@ -184,12 +185,23 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     attention_output = linear(attention_output, 'self_attn.o_proj.weight')
     # residual + attention_output, then the post-attention RMSNorm (one launch on GPU)
     residual, states = add_rms_norm(residual, attention_output, weights['post_attention_layernorm.weight'], eps)
+    # Prefill rows: silu(gate) * up in the fused gate_up GEMM's epilogue and
+    # the residual add in the down GEMM's (bit-identical to the separate ops).
+    epilogue = getattr(linear_backend, 'linear_epilogue', None)
+    activated = None
     if linear_backend is not None and _has_prepared(weights, GATE_UP_FUSED):
-        activated = _native.silu_mul(linear(states, GATE_UP_FUSED).contiguous())
+        if epilogue is not None:
+            activated = epilogue(states, weights, GATE_UP_FUSED, _native.EPI_SILU_MUL)
+        if activated is None:
+            activated = _native.silu_mul(linear(states, GATE_UP_FUSED).contiguous())
     else:
         gate = linear(states, 'mlp.gate_proj.weight')
         up = linear(states, 'mlp.up_proj.weight')
         activated = F.silu(gate) * up
+    if epilogue is not None:
+        out = epilogue(activated, weights, 'mlp.down_proj.weight', _native.EPI_RESIDUAL, residual)
+        if out is not None:
+            return out
     mlp_output = linear(activated, 'mlp.down_proj.weight')
     return residual + mlp_output
 

@@ -415,6 +415,41 @@ class CompressedLinearBackend:
                         layer[part + '._prepared'] = kind(q[r0:r0 + p.n], sc[r0:r0 + p.n], p.k, p.n)
                         r0 += p.n
 
+    def linear_epilogue(self, inputs: torch.Tensor, weights: dict, name: str, mode: int,
+                        residual: torch.Tensor | None = None) -> torch.Tensor | None:
+        """``linear`` with the MLP's next elementwise op in the prefill GEMM's
+        epilogue, bit-identical to ``linear`` followed by that op:
+        ``_native.EPI_SILU_MUL`` gives ``silu(gate) * up`` of a fused
+        ``[gate | up]`` weight, ``_native.EPI_RESIDUAL`` gives
+        ``residual + linear``.  Returns None where no such launch exists (INT8
+        weights, the decode GEMV's row counts, grids without the epilogue);
+        the caller then runs ``linear`` and the op as two steps.  Row chunks
+        follow ``marlin_max_rows_per_call`` as in ``linear``."""
+        if self.name not in FUSED_BACKENDS:
+            return None
+        prepared = weights.get(name.removesuffix('.weight') + '._prepared')
+        if not isinstance(prepared, PreparedW4):
+            return None
+        k, n, g = prepared.k, prepared.n, prepared.group_size
+        x = inputs.reshape(-1, k)
+        rows = x.shape[0]
+        step = self.marlin_max_rows_per_call if 0 < self.marlin_max_rows_per_call < rows else rows
+        if rows == 0 or not all(_native.w4a16_epilogue_supported(min(step, rows - r), n, k, g, mode)
+                                for r in range(0, rows, step)):
+            return None
+        n_out = n // 2 if mode == _native.EPI_SILU_MUL else n
+        res = residual.reshape(rows, n).contiguous() if residual is not None else None
+        self.calls += 1
+        with nvtx_range(f'weight_quant::{self.name}::{name}+epilogue{mode}'):
+            x = x.contiguous()
+            out = x.new_empty((rows, n_out))
+            for r in range(0, rows, step):
+                e = min(r + step, rows)
+                self.gemm_calls += 1
+                _native.w4a16_linear_epilogue(x[r:e], prepared.tiles, prepared.meta, n, g, mode,
+                                              None if res is None else res[r:e], out=out[r:e])
+        return out.reshape(*inputs.shape[:-1], n_out)
+
     def linear(self, inputs: torch.Tensor, weights: dict, name: str) -> torch.Tensor:
         self.calls += 1
         prefix = name.removesuffix('.weight')
