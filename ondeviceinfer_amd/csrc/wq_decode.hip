@@ -425,8 +425,9 @@ size_t attention_workspace_bytes(int64_t H, int64_t KV, int64_t max_seq) {
 // a fused [q | k | v] projection at positions start .. start + tokens - 1:
 // per (token, head) one wave (lane l holds d = 2l, 2l+1) applies the head's
 // RMSNorm and RoPE with norm_rope_pair (q and k), writes q token-major as
-// [token][head][d] (attention reads it as a strided [head][token][d] view)
-// and appends k and v to the cache rows.
+// [token][head][d], the layout prefill_attention_kernel reads (and torch's
+// SDPA as a strided [head][token][d] view), and appends k and v to the cache
+// rows.
 // grid = (tokens, ceil((q_heads + 2 kv_heads) / 4)), 256 threads.
 __global__ __launch_bounds__(256) void prefill_qk_rope_kernel(const half_t* __restrict__ qkv, int T, int H, int KV,
                                                               const half_t* __restrict__ qn_w,
