@@ -28,6 +28,8 @@ Also in the same JSON line:
 * ``prefill``: the M=4096 W4A16 GEMM per shape, TFLOP/s, next
   to the vendor library's dense fp16 GEMM (torch.matmul -> hipBLASLt, no
   dequantization) on the same shape for context;
+* ``prefill_attention``: the 4096-token prompt's causal GQA attention
+  kernel per layer, TFLOP/s, next to torch's fused SDPA for context;
 * ``batch_sweep``: fused QKV, fused gate_up and a W4 lm_head at
   M in {1, 8, 32, 128, 512}, GB/s and TFLOP/s per launch;
 * ``int8``: configs[0]'s INT8 weight shape on the GPU over a pool of 40
@@ -545,6 +547,31 @@ def main() -> int:
                             'speed_vs_vendor_fp16': round(vsec / sec, 3)})
             del g, gv, yp, wt
         result['prefill'] = prefill
+
+        # The 4096-token prompt's causal GQA attention (wq_prefill_attention:
+        # token-major q, cache rows read in place), TFLOP/s over the causal
+        # flops 4*T^2*d*H/2, beside torch's fused SDPA on the same tensors (the
+        # path it replaces; context, not a target).
+        from ondeviceinfer_amd.attention import strided_prefill_attention
+        hq, kvh, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        qa = torch.randn(PROMPT, hq, hd, device=device).half()
+        ka, va = (torch.randn(kvh, PROMPT, hd, device=device).half() for _ in range(2))
+        oa = torch.empty(PROMPT, hq, hd, device=device, dtype=torch.float16)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            native.prefill_attention(qa, hq, kvh, ka, va, 0, hd ** -0.5, out=oa)
+        sec = time_graph(torch, g, 10)
+        gs = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gs):
+            strided_prefill_attention(qa.transpose(0, 1).unsqueeze(0), ka[None], va[None])
+        ssec = time_graph(torch, gs, 10)
+        flops = 4 * PROMPT * PROMPT * hd * hq / 2
+        result['prefill_attention'] = {
+            'op': 'causal GQA flash attention (wq_prefill_attention), one layer',
+            'shape': f'T={PROMPT}, {hq}/{kvh} heads x {hd}', 'us': round(sec * 1e6, 1),
+            'tflops': round(flops / sec / 1e12, 1), 'frac_fp16_mfma': round(flops / sec / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4),
+            'torch_sdpa_us': round(ssec * 1e6, 1), 'torch_sdpa_tflops': round(flops / ssec / 1e12, 1)}
+        del g, gs, qa, ka, va, oa
 
         # fused QKV and gate_up (every layer's weights in one graph,
         # so the 256 MB Infinity Cache cannot serve repeats) and a W4 lm_head
