@@ -94,6 +94,33 @@ def test_two_layers_at_14b_geometry_match_oracle(gpu):
                 f'V cache layer {layer}')
 
 
+def test_prefill_mlp_epilogues_bit_identical_at_14b_geometry(gpu):
+    """The prefill MLP through the GEMM epilogues (silu(gate) * up in the
+    fused gate_up GEMM, the residual add in the down GEMM) gives every row's
+    logits bit for bit as the gate_up GEMM + silu_mul and the down GEMM + the
+    fp16 add do."""
+    cfg = _cfg(2)
+    print('[14b-2l epilogue] building the model', flush=True)
+    store, model, backend = _model(cfg, gpu)
+    prompt = torch.from_numpy(np.random.default_rng(7).integers(0, cfg.vocab_size, 512))[None].to(gpu)
+    taken = []
+    fused = backend.linear_epilogue
+
+    def counting(*args, **kwargs):
+        out = fused(*args, **kwargs)
+        taken.append(out is not None)
+        return out
+
+    backend.linear_epilogue = counting
+    a = model(prompt, cache=model.make_resident_cache(batch_size=1, max_seq_len=520), logits_to_keep=0).logits
+    assert taken == [True] * (2 * cfg.num_hidden_layers)     # gate_up and down of every layer
+    backend.linear_epilogue = lambda *args, **kwargs: None    # the two-step path
+    b = model(prompt, cache=model.make_resident_cache(batch_size=1, max_seq_len=520), logits_to_keep=0).logits
+    torch.cuda.synchronize()
+    assert a.shape == (1, 512, cfg.vocab_size)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_int8_two_layers_at_14b_geometry_match_oracle(gpu):
     """The INT8 weight-only model (INT8 v1 tensors, ``linear_backend=None``)
     at the same geometry: a 512-token prefill through the W8A16 GEMMs, then
