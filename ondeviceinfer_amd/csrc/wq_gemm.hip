@@ -157,10 +157,11 @@ __device__ __forceinline__ void gemm_store(const float4_t (&acc)[NT][MT], int ti
 }
 
 // Epilogue of the fused modes (W4): lane holds D[n = 4*kb + v][m = i] as above.
+// y may alias res (an in-place residual add): each element is read and then
+// written by the same lane, so neither pointer is restrict.
 template <Epi EP, int NT, int MT>
 __device__ __forceinline__ void gemm_store_epi(const float4_t (&acc)[NT][MT], int tile0, int ntile, int m0, int M,
-                                               int N, int i, int kb, const half_t* __restrict__ res,
-                                               half_t* __restrict__ y) {
+                                               int N, int i, int kb, const half_t* res, half_t* y) {
   constexpr int NO = EP == Epi::SiluPair ? NT / 2 : NT;   // output tiles per wave
   const int nout = EP == Epi::SiluPair ? N / 2 : N;
   const int nt_out = EP == Epi::SiluPair ? ntile / 2 : ntile;
@@ -211,8 +212,8 @@ template <GFmt F, int NT, int MT, Epi EP = Epi::Plain>
 __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restrict__ x, int M, int K,
                                                          const void* __restrict__ wsrc,
                                                          const void* __restrict__ wmeta, int N, int bpg,
-                                                         const half_t* __restrict__ bias, half_t* __restrict__ y, int rpx,
-                                                         int w8_tiled, const half_t* __restrict__ res) {
+                                                         const half_t* __restrict__ bias, half_t* y, int rpx,
+                                                         int w8_tiled, const half_t* res) {
   static_assert(EP == Epi::Plain || F == GFmt::W4, "fused epilogues are W4 only");
   static_assert(EP != Epi::SiluPair || NT % 2 == 0, "SiluPair pairs gate and up tiles");
   constexpr int BM = MT * 16;
