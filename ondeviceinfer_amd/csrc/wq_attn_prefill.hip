@@ -276,6 +276,14 @@ extern "C" int wq_prefill_attention(const uint16_t* q, int64_t tokens, int64_t q
   WQ_REQUIRE(start >= 0 && start + tokens <= max_seq && max_seq <= 0x7fffffff, WQ_ERR_INVALID_ARGUMENT,
              "KV cache rows %lld .. %lld exceed its %lld rows", (long long)start, (long long)(start + tokens),
              (long long)max_seq);
+  // One kv head's cache rows are read through a buffer of at most 2^31 - 1 bytes.
+  WQ_REQUIRE(max_seq * kPD * 2 <= 0x7fffffff, WQ_ERR_UNSUPPORTED,
+             "prefill attention reads at most %lld cache rows per kv head (max_seq %lld)",
+             (long long)(0x7fffffff / (kPD * 2)), (long long)max_seq);
+  // The online softmax takes the block maximum of the raw scores as the
+  // maximum of the scaled ones, which needs a positive scale.
+  WQ_REQUIRE(scale > 0.f && scale < INFINITY, WQ_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)",
+             (double)scale);
   const int64_t nqb = (tokens + kPBM - 1) / kPBM;
   WQ_REQUIRE(nqb * q_heads <= 0x7fffffff, WQ_ERR_UNSUPPORTED, "too many query blocks");
   WQ_REQUIRE(q && key_cache && value_cache && out, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");

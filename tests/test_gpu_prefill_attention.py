@@ -80,3 +80,11 @@ def test_prefill_attention_rejects_capacity_overflow(nat):
     q = torch.zeros(10, 40, 128, dtype=torch.float16, device='cuda')
     with pytest.raises(ValueError, match='exceed'):
         nat.prefill_attention(q, 40, 8, kd, kd, 60, 0.1)
+
+
+def test_prefill_attention_rejects_non_positive_scale(nat):
+    kd = torch.zeros(8, 64, 128, dtype=torch.float16, device='cuda')
+    q = torch.zeros(10, 40, 128, dtype=torch.float16, device='cuda')
+    for bad in (0.0, -0.1, float('inf')):
+        with pytest.raises(ValueError, match='scale'):
+            nat.prefill_attention(q, 40, 8, kd, kd, 0, bad)
