@@ -423,12 +423,14 @@ size_t attention_workspace_bytes(int64_t H, int64_t KV, int64_t max_seq) {
 
 // Prefill counterpart of the decode kernel's prologue, for `tokens` rows of
 // a fused [q | k | v] projection at positions start .. start + tokens - 1:
-// per (token, head) one wave (lane l holds d = 2l, 2l+1) applies the head's
-// RMSNorm and RoPE with norm_rope_pair (q and k), writes q token-major as
+// for each (token, head) a wave (lane l holds d = 2l, 2l+1) applies the
+// head's RMSNorm and RoPE with norm_rope_pair (q and k), writes q token-major as
 // [token][head][d], the layout prefill_attention_kernel reads (and torch's
 // SDPA as a strided [head][token][d] view), and appends k and v to the cache
 // rows.
-// grid = (tokens, ceil((q_heads + 2 kv_heads) / 4)), 256 threads.
+// grid = tokens, 256 threads: wave w of token t's workgroup takes heads w,
+// w + 4, ... with four head rows in flight (one workgroup per (token, four
+// heads) left the waves too little to keep in flight).
 __global__ __launch_bounds__(256) void prefill_qk_rope_kernel(const half_t* __restrict__ qkv, int T, int H, int KV,
                                                               const half_t* __restrict__ qn_w,
                                                               const half_t* __restrict__ kn_w, float eps,
@@ -437,25 +439,40 @@ __global__ __launch_bounds__(256) void prefill_qk_rope_kernel(const half_t* __re
                                                               half_t* __restrict__ kc, half_t* __restrict__ vc,
                                                               int max_seq, half_t* __restrict__ q_out) {
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x;
-  const int hh = blockIdx.y * 4 + (threadIdx.x >> 6);
-  if (hh >= H + 2 * KV) return;
-  const size_t row = (size_t)t * (H + 2 * KV) * kHeadDim;
-  const half2_t v = as_h2(reinterpret_cast<const uint32_t*>(qkv + row + (size_t)hh * kHeadDim)[lane]);
-  if (hh >= H + KV) {
-    const int h = hh - H - KV;
-    reinterpret_cast<uint32_t*>(vc + ((size_t)h * max_seq + start + t) * kHeadDim)[lane] = as_u32(v);
-    return;
-  }
-  const bool is_q = hh < H;
-  const half_t* nw_p = is_q ? qn_w : kn_w;
-  const half2_t nw = nw_p ? as_h2(reinterpret_cast<const uint32_t*>(nw_p)[lane]) : half2_t{};
+  const int NH = H + 2 * KV;
+  const half_t* src = qkv + (size_t)t * NH * kHeadDim;
+  // The token's cos / sin row and the norm weights, once per wave.
   const half2_t c2 = as_h2(reinterpret_cast<const uint32_t*>(cos_t + (size_t)t * kHeadDim)[lane]);
   const half2_t s2 = as_h2(reinterpret_cast<const uint32_t*>(sin_t + (size_t)t * kHeadDim)[lane]);
-  const half2_t r = norm_rope_pair(v, nw_p != nullptr, nw, eps, c2, s2, lane);
-  half_t* dst = is_q ? q_out + ((size_t)t * H + hh) * kHeadDim
-                     : kc + ((size_t)(hh - H) * max_seq + start + t) * kHeadDim;
-  reinterpret_cast<uint32_t*>(dst)[lane] = as_u32(r);
+  const half2_t nq = qn_w ? as_h2(reinterpret_cast<const uint32_t*>(qn_w)[lane]) : half2_t{};
+  const half2_t nk = kn_w ? as_h2(reinterpret_cast<const uint32_t*>(kn_w)[lane]) : half2_t{};
+  // Wave w takes heads w, w + 4, ...; four head rows in flight at a time.
+  constexpr int kAhead = 4;
+  for (int h0 = wave; h0 < NH; h0 += 4 * kAhead) {
+    uint32_t v[kAhead];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int hh = min(h0 + 4 * u, NH - 1);
+      v[u] = reinterpret_cast<const uint32_t*>(src + (size_t)hh * kHeadDim)[lane];
+    }
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int hh = h0 + 4 * u;   // wave-uniform
+      if (hh >= NH) break;
+      if (hh >= H + KV) {
+        reinterpret_cast<uint32_t*>(vc + ((size_t)(hh - H - KV) * max_seq + start + t) * kHeadDim)[lane] = v[u];
+        continue;
+      }
+      const bool is_q = hh < H;
+      const bool has_w = (is_q ? qn_w : kn_w) != nullptr;
+      const half2_t r = norm_rope_pair(as_h2(v[u]), has_w, is_q ? nq : nk, eps, c2, s2, lane);
+      half_t* dst = is_q ? q_out + ((size_t)t * H + hh) * kHeadDim
+                         : kc + ((size_t)(hh - H) * max_seq + start + t) * kHeadDim;
+      reinterpret_cast<uint32_t*>(dst)[lane] = as_u32(r);
+    }
+  }
 }
 
 int attention_shape_check(int64_t H, int64_t KV, int64_t head_dim, int64_t max_seq) {
@@ -590,8 +607,7 @@ extern "C" int wq_prefill_qk_rope(const uint16_t* qkv, int64_t tokens, int64_t q
   WQ_REQUIRE(((uintptr_t)qkv | (uintptr_t)cos_rows | (uintptr_t)sin_rows | (uintptr_t)key_cache |
               (uintptr_t)value_cache | (uintptr_t)q_out | (uintptr_t)q_norm_weight | (uintptr_t)k_norm_weight) % 4 == 0,
              WQ_ERR_INVALID_ARGUMENT, "operands must be 4-byte aligned");
-  const dim3 grid((unsigned)tokens, (unsigned)((q_heads + 2 * kv_heads + 3) / 4));
-  hipLaunchKernelGGL(prefill_qk_rope_kernel, grid, dim3(256), 0, as_stream(stream),
+  hipLaunchKernelGGL(prefill_qk_rope_kernel, dim3((unsigned)tokens), dim3(256), 0, as_stream(stream),
                      reinterpret_cast<const half_t*>(qkv), (int)tokens, (int)q_heads, (int)kv_heads,
                      reinterpret_cast<const half_t*>(q_norm_weight), reinterpret_cast<const half_t*>(k_norm_weight),
                      eps, reinterpret_cast<const half_t*>(cos_rows), reinterpret_cast<const half_t*>(sin_rows),
