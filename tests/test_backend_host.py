@@ -90,6 +90,31 @@ def test_row_split_dispatch_preserves_shape_and_counts():
     assert backend.calls == c['expected_calls'] and backend.gemm_calls == c['expected_gemm_calls']
 
 
+def test_linear_epilogue_dispatch_on_the_host():
+    """``linear_epilogue`` takes the fused prefill GEMM only for prepared W4
+    weights on the GEMM grids that carry the epilogue (the predicate is host
+    logic in the library, no GPU call); otherwise it returns None and the
+    decoder runs the linear and the elementwise op as two steps."""
+    from ondeviceinfer_amd import _native
+    silu, res = _native.EPI_SILU_MUL, _native.EPI_RESIDUAL
+    sup = _native.w4a16_epilogue_supported
+    assert sup(4096, 34816, 5120, 128, silu) and sup(4096, 5120, 17408, 128, res)
+    assert sup(65, 34816, 1024, 128, silu) and not sup(64, 34816, 1024, 128, silu)   # decode GEMV rows
+    assert not sup(4096, 2040, 512, 128, silu)                  # n % 32: gate and up not whole tiles
+    assert sup(2560, 1024, 1024, 128, res) and not sup(2560, 1024, 1024, 128, silu)   # one tile per wave
+    assert not sup(200, 1024, 1024, 128, res)                   # deep-ring grid
+    assert not sup(4096, 5120, 5120, 64, res) and not sup(4096, 5120, 5120, 128, 3)
+    x = torch.zeros(64, 64)
+    assert wq.CompressedLinearBackend('reference_int4').linear_epilogue(
+        x, {}, 'mlp.down_proj.weight', res, x) is None
+    backend = wq.CompressedLinearBackend('marlin')
+    w8 = {'mlp.down_proj._prepared': wq.PreparedW8(None, None, 64, 64)}
+    assert backend.linear_epilogue(x, w8, 'mlp.down_proj.weight', res, x) is None
+    w4 = {'mlp.gate_up_proj._prepared': wq.PreparedW4(None, None, None, 5120, 34816, 128)}
+    assert backend.linear_epilogue(torch.zeros(64, 5120), w4, 'mlp.gate_up_proj.weight', silu) is None
+    assert backend.calls == 0 and backend.gemm_calls == 0
+
+
 def test_no_cpu_path():
     weights, _ = synth.w4_case(16, 256, 1, name='p.weight')
     layer = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in weights.items()}
