@@ -118,6 +118,31 @@ def _has_prepared(weights: Mapping, name: str) -> bool:
     return name.removesuffix('.weight') + '._prepared' in weights
 
 
+def _int8_fused_linear(inputs: Tensor, weights: Mapping, name: str, parts: int,
+                       stats: QuantizedComputeStats | None) -> Tensor | None:
+    """The fused q|k|v or gate|up INT8 weight of a layer bound for the decode
+    graph (``_bind_int8_v1``) as one W8A16 linear, counted as its ``parts``
+    reference linears; None when the layer holds no such weight.  Each
+    output column is the same sum the per-projection linear computes."""
+    from .weight_quantization.backend import PreparedW8
+    p = weights.get(name.removesuffix('.weight') + '._prepared')
+    if not isinstance(p, PreparedW8) or not inputs.is_cuda:
+        return None
+    if stats is not None:
+        stats.linear_calls += parts
+    x = inputs.reshape(-1, p.k)
+    with nvtx_range(f'w8a16_linear::{name}'):
+        if stats is not None and stats.enabled:
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            y = _native.w8a16_linear(x, p.qweight, p.scale)
+            end.record()
+            stats.gemm_events.append((start, end))
+        else:
+            y = _native.w8a16_linear(x, p.qweight, p.scale)
+    return y.reshape(*inputs.shape[:-1], p.n)
+
+
 def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str, Tensor], config: object,
                                     layer_idx: int, cos: Tensor, sin: Tensor, scratch: Tensor, *,
                                     cache: KVCache | None = None, stats: QuantizedComputeStats | None = None,
@@ -128,7 +153,8 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     prepared fused QKV / gate_up weights (``fuse_projections``) the three and
     the two projections run as one linear each, and ``silu(gate) * up`` runs
     as one HIP kernel; on the prefill GEMM it and the MLP's residual add run
-    in the gate_up and down GEMMs' epilogues.  With a resident batch-1 cache the q/k norms, RoPE and
+    in the gate_up and down GEMMs' epilogues.  INT8 layers bound for the
+    decode graph run their fused q|k|v and gate|up W8A16 weights the same way.  With a resident batch-1 cache the q/k norms, RoPE and
     cache append run as one HIP kernel and the causal attention as another
     (``wq_prefill_attention``, reading the cache rows in place).
     """
@@ -145,6 +171,8 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     qkv = None
     if linear_backend is not None and _has_prepared(weights, QKV_FUSED):
         qkv = linear(states, QKV_FUSED)
+    elif linear_backend is None:
+        qkv = _int8_fused_linear(states, weights, QKV_FUSED, 3, stats)
     if (qkv is not None and batch_size == 1 and d == 128 and qkv.is_cuda and qkv.dtype == torch.float16
             and isinstance(cache, ResidentKVCache) and cache.batch_size == 1
             and cos.dtype == torch.float16 and tuple(cos.shape) == (1, query_length, d)):
@@ -194,6 +222,9 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
             activated = epilogue(states, weights, GATE_UP_FUSED, _native.EPI_SILU_MUL)
         if activated is None:
             activated = _native.silu_mul(linear(states, GATE_UP_FUSED).contiguous())
+    elif linear_backend is None and (gate_up := _int8_fused_linear(states, weights, GATE_UP_FUSED, 2,
+                                                                      stats)) is not None:
+        activated = _native.silu_mul(gate_up.contiguous())
     else:
         gate = linear(states, 'mlp.gate_proj.weight')
         up = linear(states, 'mlp.up_proj.weight')
