@@ -171,6 +171,21 @@ int wq_w4a16_linear_epilogue(const uint16_t* x, int64_t m, int64_t k, const void
                              int64_t n, int64_t group_size, int32_t mode, const uint16_t* residual,
                              uint16_t* y, void* stream);
 
+/* Whether wq_w8a16_linear_epilogue applies (1) or not (0): INT8 tiles
+ * (k % 128 == 0), m above 64 rows, on the prefill GEMM grids that carry a
+ * fused epilogue (mode 1: two tiles per wave and n % 32 == 0). */
+int wq_w8a16_epilogue_supported(int64_t m, int64_t n, int64_t k, int32_t mode);
+
+/* wq_w4a16_linear_epilogue for an INT8 weight in the tile layout
+ * (wq_w8_repack) with fp16 per-row scale: the linear's output is
+ * fp16(sum * scale[n]) as in wq_w8a16_linear_tiled, then mode 1 (fused
+ * [gate | up] weight and scale, output [m, n / 2]) or mode 2 (+ residual, y may
+ * alias it), bit-identical to wq_w8a16_linear_tiled followed by wq_silu_mul or
+ * the fp16 add.  Replaces the same elementwise ops of the INT8 model's
+ * prefill (quantized_model.py:216-228). */
+int wq_w8a16_linear_epilogue(const uint16_t* x, int64_t m, int64_t k, const void* tiles, const uint16_t* scale,
+                             int64_t n, int32_t mode, const uint16_t* residual, uint16_t* y, void* stream);
+
 /* ------------------------------------------------- W8 (int8, per-output-channel scale) */
 
 /* fp16 [n, k] = fp16(q * scale[n]), scale fp32 [n].  Replaces the INT8 branch

@@ -53,6 +53,8 @@ _SIGNATURES = {
     'wq_w4a16_linear_noalloc': [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _P],
     'wq_w4a16_epilogue_supported': [_I64, _I64, _I64, _I64, ctypes.c_int32],
     'wq_w4a16_linear_epilogue': [_P, _I64, _I64, _P, _P, _I64, _I64, ctypes.c_int32, _P, _P, _P],
+    'wq_w8a16_epilogue_supported': [_I64, _I64, _I64, ctypes.c_int32],
+    'wq_w8a16_linear_epilogue': [_P, _I64, _I64, _P, _P, _I64, ctypes.c_int32, _P, _P, _P],
     'wq_w4a16_decode_fused': [_P, _I64, _P, _P, _I64, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P,
                               _P, _P, ctypes.c_size_t, _P],
     'wq_w8a16_decode_fused': [_P, _I64, _P, _P, _I64, ctypes.c_int32, _P, _P, _I64, ctypes.c_float, _P, _P, _P, _P,
@@ -371,6 +373,50 @@ def w4a16_linear_epilogue(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tens
         if not out.is_contiguous() or out.data_ptr() % 16:
             raise ValueError('out must be contiguous and 16-byte aligned')
     _call('wq_w4a16_linear_epilogue', _ptr(x), m, k, _ptr(tiles), _ptr(meta), n, group_size, mode, res_ptr,
+          _ptr(out), _stream(device))
+    return out
+
+
+def w8a16_epilogue_supported(m: int, n: int, k: int, mode: int) -> bool:
+    """Whether ``w8a16_linear_epilogue`` runs this shape (INT8 tiles, m > 64,
+    the prefill GEMM grids that carry a fused epilogue)."""
+    return bool(load().wq_w8a16_epilogue_supported(m, n, k, mode))
+
+
+def w8a16_linear_epilogue(x: torch.Tensor, qweight: 'W8Tiles', scale: torch.Tensor, mode: int,
+                          residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``w4a16_linear_epilogue`` for an INT8 weight as ``W8Tiles`` with fp16
+    per-row ``scale``: bit-identical to ``w8a16_linear`` followed by
+    ``silu_mul`` (``EPI_SILU_MUL``, fused ``[gate | up]`` weight) or the fp16
+    residual add (``EPI_RESIDUAL``)."""
+    n, k, q, tiled = _w8_weight(qweight)
+    if not tiled:
+        raise ValueError('the INT8 GEMM epilogue streams W8Tiles (wq_w8_repack)')
+    device = _require_gpu(x, q, scale, residual, out)
+    if x.dtype != torch.float16 or x.dim() != 2 or x.shape[1] != k:
+        raise TypeError(f'x must be a 2-D float16 tensor with {k} features, got {x.dtype} {tuple(x.shape)}')
+    if scale.dtype != torch.float16 or scale.numel() != n:
+        raise ValueError(f'scale must be float16 with {n} entries')
+    if mode not in (EPI_SILU_MUL, EPI_RESIDUAL):
+        raise ValueError(f'mode must be EPI_SILU_MUL or EPI_RESIDUAL, got {mode}')
+    m = x.shape[0]
+    n_out = n // 2 if mode == EPI_SILU_MUL else n
+    x = _aligned(x.contiguous())
+    res_ptr = None
+    if mode == EPI_RESIDUAL:
+        if residual is None:
+            raise ValueError('EPI_RESIDUAL needs a residual tensor')
+        _check(residual, torch.float16, (m, n), 'residual')
+        if residual.data_ptr() % 8:
+            raise ValueError('residual must be 8-byte aligned')
+        res_ptr = residual.data_ptr()
+    if out is None:
+        out = torch.empty((m, n_out), dtype=torch.float16, device=device)
+    else:
+        _check(out, torch.float16, (m, n_out), 'out')
+        if out.data_ptr() % 16:
+            raise ValueError('out must be 16-byte aligned')
+    _call('wq_w8a16_linear_epilogue', _ptr(x), m, k, _ptr(q), _ptr(scale.contiguous()), n, mode, res_ptr,
           _ptr(out), _stream(device))
     return out
 

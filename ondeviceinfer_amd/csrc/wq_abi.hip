@@ -29,9 +29,11 @@ int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const ui
 int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
                    half_t* y, hipStream_t s, int tiled);
 bool w4_gemm_small_fits(int64_t M, int64_t N);
-int w4_gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode);
+int gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode, int64_t block_bytes);
 int launch_w4_gemm_epi(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                        int mode, const half_t* res, half_t* y, hipStream_t s);
+int launch_w8_gemm_epi(const half_t* x, int M, int K, const int8_t* tiles, const half_t* scale, int N, int mode,
+                       const half_t* res, half_t* y, hipStream_t s);
 int launch_w4_gemm_small(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                          half_t* y, hipStream_t s);
 
@@ -135,7 +137,15 @@ bool w4_epilogue_fits(int64_t m, int64_t n, int64_t k, int64_t group_size, int32
   if (m <= kSkinnyMaxM || w4_gemm_small_fits(m, n) || k > kGemmMaxK) return false;
   if (n % (mode == 1 ? 32 : 8) != 0 || group_size <= 0 || group_size % kW4BlockK != 0 || k % group_size != 0)
     return false;
-  return w4_gemm_epi_plan(m, n, k, mode) != 0;
+  return gemm_epi_plan(m, n, k, mode, 1024) != 0;
+}
+
+// The same for INT8 tiles (k % 128 == 0).
+bool w8_epilogue_fits(int64_t m, int64_t n, int64_t k, int32_t mode) {
+  if (mode != 1 && mode != 2) return false;
+  if (m <= kSkinnyMaxM || k > kGemmMaxK || k % kW8BlockK != 0) return false;
+  if (n % (mode == 1 ? 32 : 8) != 0) return false;
+  return gemm_epi_plan(m, n, k, mode, kW8TileBlockBytes) != 0;
 }
 }  // namespace
 
@@ -160,6 +170,29 @@ extern "C" int wq_w4a16_linear_epilogue(const uint16_t* x, int64_t m, int64_t k,
   return launch_w4_gemm_epi(reinterpret_cast<const half_t*>(x), (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
                             reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size,
                             mode, reinterpret_cast<const half_t*>(residual), reinterpret_cast<half_t*>(y),
+                            as_stream(stream));
+}
+
+extern "C" int wq_w8a16_epilogue_supported(int64_t m, int64_t n, int64_t k, int32_t mode) {
+  if (linear_shape_check(m, n, k) != WQ_OK) return 0;
+  return w8_epilogue_fits(m, n, k, mode) ? 1 : 0;
+}
+
+extern "C" int wq_w8a16_linear_epilogue(const uint16_t* x, int64_t m, int64_t k, const void* tiles,
+                                        const uint16_t* scale, int64_t n, int32_t mode, const uint16_t* residual,
+                                        uint16_t* y, void* stream) {
+  if (int st = linear_shape_check(m, n, k)) return st;
+  WQ_REQUIRE(mode == 1 || mode == 2, WQ_ERR_INVALID_ARGUMENT, "mode must be 1 (silu_mul) or 2 (residual)");
+  WQ_REQUIRE(w8_epilogue_fits(m, n, k, mode), WQ_ERR_UNSUPPORTED,
+             "W8A16 epilogue mode %d does not apply to m=%lld n=%lld k=%lld (see wq_w8a16_epilogue_supported)",
+             (int)mode, (long long)m, (long long)n, (long long)k);
+  WQ_REQUIRE(x && y && tiles && scale && (mode == 1 || residual), WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(aligned16(x) && aligned16(tiles) && aligned16(y) &&
+                 (mode == 1 || (reinterpret_cast<uintptr_t>(residual) & 7u) == 0),
+             WQ_ERR_INVALID_ARGUMENT, "x, tiles and y must be 16-byte aligned and residual 8-byte aligned");
+  return launch_w8_gemm_epi(reinterpret_cast<const half_t*>(x), (int)m, (int)k, reinterpret_cast<const int8_t*>(tiles),
+                            reinterpret_cast<const half_t*>(scale), (int)n, mode,
+                            reinterpret_cast<const half_t*>(residual), reinterpret_cast<half_t*>(y),
                             as_stream(stream));
 }
 

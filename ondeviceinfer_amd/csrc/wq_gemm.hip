@@ -148,6 +148,11 @@ __device__ __forceinline__ void gemm_store(const float4_t (&acc)[NT][MT], int ti
           if (n < N) {
             float r = acc[t][mt][v] * (float)scale[n];
             if (bias) r += (float)bias[n];
+            // A plain fp32 result, then one conversion: left alone, hipcc may
+            // fold the product and the conversion into one mixed-precision
+            // FMA that rounds straight to fp16, which the fused epilogues
+            // (gemm_store_epi) could not match bit for bit.
+            asm("" : "+v"(r));
             y[(size_t)m * N + n] = (half_t)r;
           }
         }
@@ -156,12 +161,23 @@ __device__ __forceinline__ void gemm_store(const float4_t (&acc)[NT][MT], int ti
   }
 }
 
-// Epilogue of the fused modes (W4): lane holds D[n = 4*kb + v][m = i] as above.
-// y may alias res (an in-place residual add): each element is read and then
-// written by the same lane, so neither pointer is restrict.
-template <Epi EP, int NT, int MT>
+// Epilogue of the fused modes: lane holds D[n = 4*kb + v][m = i] as above;
+// the linear's fp16 output is the sum rounded (W4) or the sum times the
+// channel scale rounded (INT8, as gemm_store).  y may alias res (an in-place
+// residual add): each element is read and then written by the same lane, so
+// neither pointer is restrict.
+template <GFmt F, Epi EP, int NT, int MT>
 __device__ __forceinline__ void gemm_store_epi(const float4_t (&acc)[NT][MT], int tile0, int ntile, int m0, int M,
-                                               int N, int i, int kb, const half_t* res, half_t* y) {
+                                               int N, int i, int kb, const void* wmeta, const half_t* res,
+                                               half_t* y) {
+  auto out16 = [&](float a, int n) -> half_t {
+    if constexpr (F == GFmt::W4) return (half_t)a;
+    else {
+      float r = a * (float)reinterpret_cast<const half_t*>(wmeta)[n];
+      asm("" : "+v"(r));   // as gemm_store: one fp32 product, then one conversion
+      return (half_t)r;
+    }
+  };
   constexpr int NO = EP == Epi::SiluPair ? NT / 2 : NT;   // output tiles per wave
   const int nout = EP == Epi::SiluPair ? N / 2 : N;
   const int nt_out = EP == Epi::SiluPair ? ntile / 2 : ntile;
@@ -177,13 +193,13 @@ __device__ __forceinline__ void gemm_store_epi(const float4_t (&acc)[NT][MT], in
       if constexpr (EP == Epi::SiluPair) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const half_t g = (half_t)acc[t][mt][v], u = (half_t)acc[t + NO][mt][v];
+          const half_t g = out16(acc[t][mt][v], n0 + v), u = out16(acc[t + NO][mt][v], nout + n0 + v);
           o[v] = (half_t)silu_f((float)g) * u;
         }
       } else {
         const half4_t r = *reinterpret_cast<const half4_t*>(res + (size_t)m * N + n0);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = (half_t)((float)(half_t)acc[t][mt][v] + (float)r[v]);
+        for (int v = 0; v < 4; ++v) o[v] = (half_t)((float)out16(acc[t][mt][v], n0 + v) + (float)r[v]);
       }
       *reinterpret_cast<half4_t*>(y + (size_t)m * nout + n0) = o;
     }
@@ -214,7 +230,6 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
                                                          const void* __restrict__ wmeta, int N, int bpg,
                                                          const half_t* __restrict__ bias, half_t* y, int rpx,
                                                          int w8_tiled, const half_t* res) {
-  static_assert(EP == Epi::Plain || F == GFmt::W4, "fused epilogues are W4 only");
   static_assert(EP != Epi::SiluPair || NT % 2 == 0, "SiluPair pairs gate and up tiles");
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kRowBytes;
@@ -289,7 +304,7 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
       const uint32_t p1 = w8_tiled ? kW8TileBlockBytes / 2 : 64;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const uint32_t so = w8_tiled ? (uint32_t)((t * nblk + blk) * kW8TileBlockBytes)
+        const uint32_t so = w8_tiled ? (uint32_t)((toff(t) * nblk + blk) * kW8TileBlockBytes)
                                      : (uint32_t)(t * 16 * K + blk * kW8BlockK);
         r.a[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo, so, kNtPolicy);
         r.b[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + p1, so, kNtPolicy);
@@ -327,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void wq_gemm_kernel(const half_t* __restric
   if constexpr (EP == Epi::Plain)
     gemm_store<F, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, wmeta, bias, y);
   else
-    gemm_store_epi<EP, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, res, y);
+    gemm_store_epi<F, EP, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, wmeta, res, y);
 }
 
 // Deep-ring form, for grids whose per-block math is short (wide N at
@@ -541,12 +556,13 @@ int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const ui
   return launch_gemm_auto<GFmt::W4>(x, M, K, tiles, meta, N, G / kW4BlockK, nullptr, y, s, 0);
 }
 
-// The grid launch_gemm_auto picks for a W4 shape, when it is a wq_gemm_kernel
+// The grid launch_gemm_auto picks for a W4 (or INT8-tile) shape, when it is a wq_gemm_kernel
 // grid that can carry a fused epilogue: 1 = NT 4 / MT 8, 2 = NT 2 / MT 4,
 // 3 = NT 1 / MT 4 (Residual only: SiluPair pairs tiles within a wave); 0
-// otherwise.  SiluPair also needs the up tiles' offsets (nh + NT tiles from
-// a wave's first tile) inside the 31-bit buffer range.
-int w4_gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode) {
+// otherwise.  SiluPair also needs the up tiles' offsets (nh + NT tiles of
+// block_bytes per 128-k block from a wave's first tile) inside the 31-bit
+// buffer range.
+int gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode, int64_t block_bytes) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128, mb64 = (M + 63) / 64;
   int plan = 0;
   if (((ntile + 15) / 16) * mblk >= 512) plan = 1;
@@ -554,7 +570,7 @@ int w4_gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode) {
   else if (((ntile + 3) / 4) * mb64 >= 384) plan = 3;
   if (mode == 1) {
     if (plan == 3 || N % 32 != 0) return 0;
-    if ((ntile / 2 + 4) * (K / kW4BlockK) * 1024 > 0x7fffffffL) return 0;
+    if ((ntile / 2 + 4) * (K / kW4BlockK) * block_bytes > 0x7fffffffL) return 0;
   }
   return plan;
 }
@@ -564,13 +580,26 @@ int w4_gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode) {
 int launch_w4_gemm_epi(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                        int mode, const half_t* res, half_t* y, hipStream_t s) {
   const int bpg = G / kW4BlockK;
-  switch (w4_gemm_epi_plan(M, N, K, mode) * 2 + (mode == 1 ? 0 : 1)) {
+  switch (gemm_epi_plan(M, N, K, mode, 1024) * 2 + (mode == 1 ? 0 : 1)) {
     case 2: return launch_gemm<GFmt::W4, 4, 8, Epi::SiluPair>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
     case 3: return launch_gemm<GFmt::W4, 4, 8, Epi::Residual>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0, res);
     case 4: return launch_gemm<GFmt::W4, 2, 4, Epi::SiluPair>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
     case 5: return launch_gemm<GFmt::W4, 2, 4, Epi::Residual>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0, res);
     case 7: return launch_gemm<GFmt::W4, 1, 4, Epi::Residual>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0, res);
     default: return fail(WQ_ERR_UNSUPPORTED, "w4 GEMM epilogue: shape has no fused-epilogue grid");
+  }
+}
+
+// The same for INT8 tiles (scale: fp16 per output row).
+int launch_w8_gemm_epi(const half_t* x, int M, int K, const int8_t* tiles, const half_t* scale, int N, int mode,
+                       const half_t* res, half_t* y, hipStream_t s) {
+  switch (gemm_epi_plan(M, N, K, mode, kW8TileBlockBytes) * 2 + (mode == 1 ? 0 : 1)) {
+    case 2: return launch_gemm<GFmt::W8, 4, 8, Epi::SiluPair>(x, M, K, tiles, scale, N, 1, nullptr, y, s, 1);
+    case 3: return launch_gemm<GFmt::W8, 4, 8, Epi::Residual>(x, M, K, tiles, scale, N, 1, nullptr, y, s, 1, res);
+    case 4: return launch_gemm<GFmt::W8, 2, 4, Epi::SiluPair>(x, M, K, tiles, scale, N, 1, nullptr, y, s, 1);
+    case 5: return launch_gemm<GFmt::W8, 2, 4, Epi::Residual>(x, M, K, tiles, scale, N, 1, nullptr, y, s, 1, res);
+    case 7: return launch_gemm<GFmt::W8, 1, 4, Epi::Residual>(x, M, K, tiles, scale, N, 1, nullptr, y, s, 1, res);
+    default: return fail(WQ_ERR_UNSUPPORTED, "INT8 GEMM epilogue: shape has no fused-epilogue grid");
   }
 }
 

@@ -143,6 +143,27 @@ def _int8_fused_linear(inputs: Tensor, weights: Mapping, name: str, parts: int,
     return y.reshape(*inputs.shape[:-1], p.n)
 
 
+def _int8_epilogue(inputs: Tensor, weights: Mapping, name: str, parts: int, stats: QuantizedComputeStats | None,
+                   mode: int, residual: Tensor | None = None) -> Tensor | None:
+    """``_int8_fused_linear`` (or a bound per-projection INT8 weight) with the
+    MLP's next elementwise op in the prefill GEMM's epilogue
+    (``_native.w8a16_linear_epilogue``); None where that launch does not apply
+    (rows at or below the decode GEMV's 64, grids without the epilogue)."""
+    from .weight_quantization.backend import PreparedW8
+    p = weights.get(name.removesuffix('.weight') + '._prepared')
+    if not isinstance(p, PreparedW8) or not isinstance(p.qweight, _native.W8Tiles) or not inputs.is_cuda:
+        return None
+    x = inputs.reshape(-1, p.k)
+    if not _native.w8a16_epilogue_supported(x.shape[0], p.n, p.k, mode):
+        return None
+    if stats is not None:
+        stats.linear_calls += parts
+    res = residual.reshape(x.shape[0], p.n).contiguous() if residual is not None else None
+    with nvtx_range(f'w8a16_linear::{name}+epilogue{mode}'):
+        y = _native.w8a16_linear_epilogue(x.contiguous(), p.qweight, p.scale, mode, res)
+    return y.reshape(*inputs.shape[:-1], y.shape[-1])
+
+
 def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str, Tensor], config: object,
                                     layer_idx: int, cos: Tensor, sin: Tensor, scratch: Tensor, *,
                                     cache: KVCache | None = None, stats: QuantizedComputeStats | None = None,
@@ -222,6 +243,9 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
             activated = epilogue(states, weights, GATE_UP_FUSED, _native.EPI_SILU_MUL)
         if activated is None:
             activated = _native.silu_mul(linear(states, GATE_UP_FUSED).contiguous())
+    elif linear_backend is None and (act := _int8_epilogue(states, weights, GATE_UP_FUSED, 2, stats,
+                                                             _native.EPI_SILU_MUL)) is not None:
+        activated = act
     elif linear_backend is None and (gate_up := _int8_fused_linear(states, weights, GATE_UP_FUSED, 2,
                                                                       stats)) is not None:
         activated = _native.silu_mul(gate_up.contiguous())
@@ -231,6 +255,10 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
         activated = F.silu(gate) * up
     if epilogue is not None:
         out = epilogue(activated, weights, 'mlp.down_proj.weight', _native.EPI_RESIDUAL, residual)
+        if out is not None:
+            return out
+    elif linear_backend is None:
+        out = _int8_epilogue(activated, weights, 'mlp.down_proj.weight', 1, stats, _native.EPI_RESIDUAL, residual)
         if out is not None:
             return out
     mlp_output = linear(activated, 'mlp.down_proj.weight')

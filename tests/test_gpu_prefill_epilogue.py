@@ -96,6 +96,52 @@ def test_residual_epilogue_equals_gemm_then_add(gpu, m, n, k):
     assert qdq.parity_ok(metrics), metrics
 
 
+def _int8_weight(n, k, seed, device):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    s = (rng.random(n) * 2e-3 + 1e-4).astype(np.float16)
+    return q, s, _native.w8_repack(_dev(q, device)), _dev(s, device)
+
+
+@pytest.mark.parametrize('m,n_half,k', [
+    (4096, 17408, 5120),    # the INT8 model's fused gate_up at the 4K prompt
+    (300, 17408, 5120),     # 128-wide slices of 64-row tiles
+    (4096, 1040, 512),      # partial last slice
+])
+def test_int8_silu_epilogue_equals_gemm_then_silu_mul(gpu, m, n_half, k):
+    print(f'[int8 epilogue silu] m={m} n_half={n_half} k={k}', flush=True)
+    q, s, tiles, scale = _int8_weight(2 * n_half, k, m + k, gpu)
+    assert _native.w8a16_epilogue_supported(m, 2 * n_half, k, _native.EPI_SILU_MUL)
+    x = torch.randn(m, k, dtype=torch.float16, device=gpu)
+    fused = _native.w8a16_linear_epilogue(x, tiles, scale, _native.EPI_SILU_MUL)
+    plain = _native.silu_mul(_native.w8a16_linear(x, tiles, scale))
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), plain.view(torch.int16))
+    rows = _rows(m)
+    xs = x[torch.from_numpy(rows).to(gpu)].cpu().numpy()
+    ref = qwen3.swiglu(qdq.int8_weight_only_linear(xs, q[:n_half], s[:n_half]),
+                       qdq.int8_weight_only_linear(xs, q[n_half:], s[n_half:]))
+    metrics = qdq.parity_metrics(fused.cpu().numpy()[rows], ref)
+    assert qdq.parity_ok(metrics), metrics
+
+
+@pytest.mark.parametrize('m,n,k', [(4096, 5120, 17408), (2560, 1024, 1024)])
+def test_int8_residual_epilogue_equals_gemm_then_add(gpu, m, n, k):
+    print(f'[int8 epilogue residual] m={m} n={n} k={k}', flush=True)
+    q, s, tiles, scale = _int8_weight(n, k, n + k, gpu)
+    assert _native.w8a16_epilogue_supported(m, n, k, _native.EPI_RESIDUAL)
+    x = torch.randn(m, k, dtype=torch.float16, device=gpu)
+    res = torch.randn(m, n, dtype=torch.float16, device=gpu) * 4
+    fused = _native.w8a16_linear_epilogue(x, tiles, scale, _native.EPI_RESIDUAL, res)
+    plain = res + _native.w8a16_linear(x, tiles, scale)
+    inplace = res.clone()
+    _native.w8a16_linear_epilogue(x, tiles, scale, _native.EPI_RESIDUAL, inplace, out=inplace)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), plain.view(torch.int16))
+    assert torch.equal(inplace.view(torch.int16), plain.view(torch.int16))
+    assert not _native.w8a16_epilogue_supported(64, n, k, _native.EPI_RESIDUAL)
+
+
 def test_epilogue_rejects_decode_rows_and_backend_falls_back(gpu):
     backend, layer, wg, wu = _gate_up(17408, 512, seed=3, device=gpu)
     p = layer['mlp.gate_up_proj._prepared']

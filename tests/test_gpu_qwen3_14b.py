@@ -121,6 +121,36 @@ def test_prefill_mlp_epilogues_bit_identical_at_14b_geometry(gpu):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+def test_int8_prefill_epilogues_bit_identical_at_14b_geometry(gpu, monkeypatch):
+    """The INT8 model's prefill MLP through the W8A16 GEMM epilogues gives
+    every row's logits bit for bit as the fused gate_up GEMM + silu_mul and
+    the down GEMM + the fp16 add do."""
+    from ondeviceinfer_amd import quantized_model as qm
+    from ondeviceinfer_amd.runtime.quantized import QuantizedResidentRuntime
+    from ondeviceinfer_amd.weight_quantization.synthetic import random_int8_store
+    cfg = _cfg(2)
+    print('[14b-int8-2l epilogue] building the model', flush=True)
+    store = random_int8_store(cfg, seed=2, device=gpu)
+    model = qm.QuantizedQwen3ForCausalLM(store, QuantizedResidentRuntime(store, device=gpu), device=gpu,
+                                         linear_backend=None)
+    prompt = torch.from_numpy(np.random.default_rng(8).integers(0, cfg.vocab_size, 512))[None].to(gpu)
+    taken = []
+    fused = qm._int8_epilogue
+
+    def counting(*args, **kwargs):
+        out = fused(*args, **kwargs)
+        taken.append(out is not None)
+        return out
+
+    monkeypatch.setattr(qm, '_int8_epilogue', counting)
+    a = model(prompt, cache=model.make_resident_cache(batch_size=1, max_seq_len=520), logits_to_keep=0).logits
+    assert taken == [True] * (2 * cfg.num_hidden_layers)
+    monkeypatch.setattr(qm, '_int8_epilogue', lambda *args, **kwargs: None)
+    b = model(prompt, cache=model.make_resident_cache(batch_size=1, max_seq_len=520), logits_to_keep=0).logits
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_int8_two_layers_at_14b_geometry_match_oracle(gpu):
     """The INT8 weight-only model (INT8 v1 tensors, ``linear_backend=None``)
     at the same geometry: a 512-token prefill through the W8A16 GEMMs, then
