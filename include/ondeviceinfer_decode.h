@@ -127,6 +127,24 @@ int wq_argmax_f16_workspace_size(int64_t n, size_t* bytes);
 int wq_argmax_f16(const uint16_t* x, int64_t n, int64_t* token, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* *device_ptr = the address kernels use for pinned host memory at host_ptr
+ * (hipHostGetDevicePointer); WQ_ERR_INVALID_ARGUMENT when host_ptr is not in
+ * a device-mapped pinned allocation.  Not a stream operation.  Used to hand
+ * wq_embed_rows the embedding table that stays in host memory, as the
+ * reference keeps it (quantized_model.py:289-291). */
+int wq_host_device_pointer(const void* host_ptr, void** device_ptr);
+
+/* out[r, :] = table[tokens[r], :] for r < rows: the embedding rows of fp16
+ * [vocab, hidden] (hidden % 8 == 0) for device int64 token ids; table may be
+ * the device address of pinned host memory (wq_host_device_pointer), read over
+ * the host link.  A token outside [0, vocab) writes NaN and reads nothing.
+ * table and out 16-byte aligned.
+ * Replaces: `F.embedding(ids_cpu, self.store.embed_tokens)` + `.to(device)`
+ * (quantized_model.py:289-291) for a token id that is already on the device
+ * (the previous decode step's greedy token). */
+int wq_embed_rows(const uint16_t* table, int64_t vocab, int64_t hidden, const int64_t* tokens, int64_t rows,
+                  uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,8 @@ _SIGNATURES = {
     'wq_argmax_f16_workspace_size': [_I64, _SIZE_P],
     'wq_argmax_f16': [_P, _I64, _P, _P, ctypes.c_size_t, _P],
     'wq_lm_head': [_P, _I64, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
+    'wq_host_device_pointer': [_P, ctypes.POINTER(ctypes.c_void_p)],
+    'wq_embed_rows': [_P, _I64, _I64, _P, _I64, _P, _P],
 }
 EXPORTED_SYMBOLS = ('wq_last_error', *_SIGNATURES)
 
@@ -857,4 +859,56 @@ def argmax_f16(x: torch.Tensor, *, out: torch.Tensor | None = None,
         workspace = shared_workspace(device, argmax_f16_workspace_size(n), ('argmax_f16', n))
     _call('wq_argmax_f16', _ptr(_aligned(x)), n, _ptr(out), workspace.data_ptr(),
           workspace.numel() * workspace.element_size(), _stream(device))
+    return out
+
+
+# ----------------------------------------------------------------------------- embedding
+
+class HostTable(NamedTuple):
+    """An fp16 ``[rows, cols]`` table kept in pinned host memory, with the
+    address kernels read it at (``wq_host_device_pointer``)."""
+    tensor: torch.Tensor     # pinned CPU fp16, contiguous
+    device_ptr: int
+    device: torch.device
+
+
+def host_table(table: torch.Tensor, device: torch.device | str) -> HostTable:
+    """``table`` (CPU fp16 2-D) in pinned host memory, mapped for ``device``'s
+    kernels; a pinned contiguous table is used as it is, anything else is
+    copied into a new pinned buffer."""
+    if table.device.type != 'cpu' or table.dtype != torch.float16 or table.dim() != 2:
+        raise ValueError(f'expected a 2-D float16 CPU table, got {table.dtype} {tuple(table.shape)} on {table.device}')
+    device = torch.device(device)
+    table = table.contiguous()
+    if not table.is_pinned():
+        table = table.pin_memory()
+    ptr = ctypes.c_void_p()
+    with torch.cuda.device(device):
+        _call('wq_host_device_pointer', table.data_ptr(), ctypes.byref(ptr))
+    return HostTable(table, int(ptr.value), device)
+
+
+def embed_rows(table: 'HostTable | torch.Tensor', tokens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out[r] = table[tokens[r]]`` (``wq_embed_rows``): the embedding rows of
+    device int64 token ids from a ``HostTable`` (read over the host link) or a
+    device fp16 table; an out-of-range id gives a NaN row."""
+    if isinstance(table, HostTable):
+        vocab, hidden = table.tensor.shape
+        tptr, tdev = table.device_ptr, table.device
+    else:
+        if table.dtype != torch.float16 or table.dim() != 2 or not table.is_contiguous():
+            raise ValueError('table must be a contiguous 2-D float16 tensor')
+        vocab, hidden = table.shape
+        tptr, tdev = table.data_ptr(), _require_gpu(table)
+    device = _require_gpu(tokens, out)
+    if device != tdev:
+        raise ValueError(f'table is mapped for {tdev}, tokens are on {device}')
+    if tokens.dtype != torch.int64 or not tokens.is_contiguous():
+        raise TypeError('tokens must be a contiguous int64 tensor')
+    rows = tokens.numel()
+    if out is None:
+        out = torch.empty((rows, hidden), dtype=torch.float16, device=device)
+    elif out.dtype != torch.float16 or out.numel() != rows * hidden or not out.is_contiguous():
+        raise ValueError(f'out must be a contiguous float16 tensor of {rows * hidden} elements')
+    _call('wq_embed_rows', tptr, vocab, hidden, _ptr(tokens), rows, _ptr(out), _stream(device))
     return out

@@ -487,10 +487,49 @@ int attention_shape_check(int64_t H, int64_t KV, int64_t head_dim, int64_t max_s
   return WQ_OK;
 }
 
+// ------------------------------------------------------------ embedding row
+// out[r] = table[token[r]] for the rows of an fp16 table that may live in
+// pinned host memory (read through its device-visible mapping, 16 bytes per
+// lane: one row of 5120 is 640 lane loads over the host link).  One
+// workgroup per row; a token outside [0, vocab) writes NaN and reads nothing.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint4_t* __restrict__ table, int64_t vocab,
+                                                         int chunks, const int64_t* __restrict__ tokens,
+                                                         uint4_t* __restrict__ out) {
+  const int64_t t = tokens[blockIdx.x];
+  const bool ok = t >= 0 && t < vocab;
+  const uint4_t nan8 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+  uint4_t* dst = out + (size_t)blockIdx.x * chunks;
+  for (int c = threadIdx.x; c < chunks; c += 256) dst[c] = ok ? table[(size_t)t * chunks + c] : nan8;
+}
+
 }  // namespace
 }  // namespace wq
 
 using namespace wq;
+
+extern "C" int wq_host_device_pointer(const void* host_ptr, void** device_ptr) {
+  WQ_REQUIRE(host_ptr && device_ptr, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  void* d = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&d, const_cast<void*>(host_ptr), 0);
+  WQ_REQUIRE(e == hipSuccess && d, WQ_ERR_INVALID_ARGUMENT,
+             "not a device-mapped pinned host allocation (hipHostGetDevicePointer: %s)", hipGetErrorString(e));
+  *device_ptr = d;
+  return WQ_OK;
+}
+
+extern "C" int wq_embed_rows(const uint16_t* table, int64_t vocab, int64_t hidden, const int64_t* tokens,
+                             int64_t rows, uint16_t* out, void* stream) {
+  if (rows == 0) return WQ_OK;
+  WQ_REQUIRE(table && tokens && out, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(vocab > 0 && hidden > 0 && hidden % 8 == 0 && hidden <= (1 << 24) && rows > 0 && rows <= 65535,
+             WQ_ERR_INVALID_ARGUMENT, "need vocab > 0, 0 < hidden, hidden %% 8 == 0, 0 < rows <= 65535");
+  WQ_REQUIRE(((uintptr_t)table | (uintptr_t)out) % 16 == 0 && (uintptr_t)tokens % 8 == 0, WQ_ERR_INVALID_ARGUMENT,
+             "table and out must be 16-byte aligned, tokens 8-byte");
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint4_t*>(table), vocab, (int)(hidden / 8), tokens,
+                     reinterpret_cast<uint4_t*>(out));
+  return check_launch("embed_rows");
+}
 
 extern "C" int wq_add_rmsnorm(const uint16_t* x, const uint16_t* delta, const uint16_t* weight, int64_t rows,
                               int64_t n, float eps, uint16_t* out_norm, uint16_t* out_sum, void* stream) {

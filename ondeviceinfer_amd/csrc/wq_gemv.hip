@@ -496,10 +496,13 @@ __global__ __launch_bounds__((64 * flat_max_ksw<NB, F>()), (flat_min_waves<NB, F
     if constexpr (XM == XMode::RmsNorm) xa[j] = *reinterpret_cast<const uint4_t*>(fz.norm_w + off);
   }
   if constexpr (XM == XMode::RmsNorm) {
-    // Unconditional (clamped) loads; entries past the count are dropped when summed.
+    // Clamped loads; entries past the count are dropped when summed.  With
+    // fewer than 4 sums there is no whole float4 to read (a uniform branch).
 #pragma unroll
     for (int u = 0; u < kSqPerLane; ++u)
-      sq[u] = reinterpret_cast<const float4_t*>(fz.sumsq_in)[max(min(lane + 64 * u, fz.sumsq_count / 4 - 1), 0)];
+      sq[u] = fz.sumsq_count >= 4
+                  ? reinterpret_cast<const float4_t*>(fz.sumsq_in)[min(lane + 64 * u, fz.sumsq_count / 4 - 1)]
+                  : float4_t{0.f, 0.f, 0.f, 0.f};
     sqt = fz.sumsq_in[min((fz.sumsq_count & ~3) + (lane & 3), fz.sumsq_count - 1)];
   }
   // The fused residual (M = 1; wave 0 stores the tile) is fetched now so

@@ -71,11 +71,13 @@ def int8_weight_only_linear(inputs: Tensor, weights: Mapping[str, Tensor], weigh
     n, k = qweight.shape
     x = inputs.reshape(-1, k)
     scale16 = scale if scale.dtype == torch.float16 else scale.half()
-    # A layer bound for the decode graph (_bind_int8_v1) also holds the same
-    # weight as INT8 tiles, which the kernels stream faster; same results.
+    # A layer bound for the decode graph (_bind_int8_v1) holds the weight as
+    # INT8 tiles, which the kernels stream faster; same results.
     prepared = weights.get(weight_name.removesuffix('.weight') + '._prepared')
     if prepared is not None and prepared.n == n and prepared.k == k:
         qweight, scale16 = prepared.qweight, prepared.scale
+    elif isinstance(qweight, TiledInt8QWeight):
+        qweight = qweight.w8_tiles
     with nvtx_range(f'w8a16_linear::{weight_name}'):
         if stats is not None and stats.enabled and inputs.device.type == 'cuda':
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -265,15 +267,47 @@ def quantized_decoder_layer_forward(hidden_states: Tensor, weights: Mapping[str,
     return residual + mlp_output
 
 
+class TiledInt8QWeight(torch.Tensor):
+    """The ``prefix.qweight`` entry of an INT8 layer whose weight is held only
+    as INT8 tiles (``_native.W8Tiles``): an int8 ``[N, K]`` tensor in shape,
+    dtype and device, with no row-major storage of its own.  Metadata
+    (``shape``, ``dtype``, ``device``, ``numel``) is answered directly, so the
+    loader's and ``int8_weight_only_linear``'s checks run unchanged; any torch
+    operation on it first rebuilds the row-major weight with ``wq_w8_unpack``
+    (a temporary ``[N, K]`` copy, bit-exact) and runs on that."""
+
+    @staticmethod
+    def __new__(cls, tiles: '_native.W8Tiles'):
+        r = torch.Tensor._make_wrapper_subclass(cls, (tiles.n, tiles.k), dtype=torch.int8,
+                                                device=tiles.tiles.device, requires_grad=False)
+        r.w8_tiles = tiles
+        return r
+
+    def __repr__(self) -> str:
+        return f'TiledInt8QWeight(shape={tuple(self.shape)}, device={self.device})'
+
+    def row_major(self) -> Tensor:
+        return _native.w8_unpack(self.w8_tiles)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        from torch.utils._pytree import tree_map
+
+        def unwrap(t):
+            return t.row_major() if isinstance(t, TiledInt8QWeight) else t
+        return func(*tree_map(unwrap, args), **tree_map(unwrap, kwargs or {}))
+
+
 def _bind_int8_v1(layer: dict, ops) -> None:
     """Give an INT8 v1 layer the prepared entries the decode graph runs:
     per linear a ``PreparedW8`` over its weight as INT8 tiles (``int8_streamed``)
     and fp16 ``scale``, then q|k|v and gate|up concatenated
-    (``fuse_projections``).  The row-major ``qweight`` / ``scale`` entries
-    stay as the reference keeps them; ``int8_weight_only_linear`` takes the
-    tiles of a bound layer (same values, same results).  When the weights
-    stay row-major (k % 128 != 0) the parts' entries are rebound to views of
-    the fused copies so that no weight is held twice."""
+    (``fuse_projections``).  The weight is then held once: each row-major
+    ``qweight`` entry is replaced by a ``TiledInt8QWeight`` over the fused
+    tiles (the reference's keys, shapes and dtypes stay; the row-major copy
+    is freed), and ``scale`` by a view of the fused scales.  When the weights
+    stay row-major (k % 128 != 0) the entries are rebound to views of the
+    fused row-major copies instead."""
     from .weight_quantization.backend import PreparedW8, int8_streamed
     if not all(qweight_name(n) in layer for n in LINEAR_WEIGHT_NAMES) or QKV_FUSED.removesuffix('.weight') + \
             '._prepared' in layer:
@@ -288,6 +322,8 @@ def _bind_int8_v1(layer: dict, ops) -> None:
         p = layer[name.removesuffix('.weight') + '._prepared']
         if isinstance(p.qweight, torch.Tensor):
             layer[qweight_name(name)] = p.qweight
+        else:
+            layer[qweight_name(name)] = TiledInt8QWeight(p.qweight)
         if layer[scale_name(name)].dtype == torch.float16:
             layer[scale_name(name)] = p.scale
 
@@ -303,9 +339,10 @@ class DecodeStepGraph:
     (W8A16) weights alike; other formats (W8A8) take the same
     steps with the norms, residual adds and SiLU*up as separate kernels.
     Inputs are the token id and the position (device
-    scalars); every launch is a HIP kernel of this library except the
-    embedding gather (torch), and the LM head falls back to torch's GEMM
-    when the hidden size is not a multiple of 512."""
+    scalars); the token's embedding row comes from the table in pinned host
+    memory (``wq_embed_rows``); every launch is a HIP kernel of this library,
+    except that the LM head falls back to torch's GEMM when the hidden size
+    is not a multiple of 512."""
 
     def __init__(self, model: 'QuantizedQwen3ForCausalLM', key_cache: list[Tensor], value_cache: list[Tensor],
                  max_seq_len: int):
@@ -345,7 +382,7 @@ class DecodeStepGraph:
             for name in (QKV_FUSED, 'self_attn.o_proj.weight', GATE_UP_FUSED, 'mlp.down_proj.weight'):
                 if not _has_prepared(w, name):
                     raise ValueError(f'decode graph needs prepared {name}')
-        self.embed = model.device_embedding()
+        self.embed = model.embedding_table()
         self.lm_head_t = model.lm_head.t()
         from .weight_quantization.backend import PreparedW4, PreparedW8
         names = ('self_attn.qkv_proj', 'self_attn.o_proj', 'mlp.gate_up_proj', 'mlp.down_proj')
@@ -392,7 +429,7 @@ class DecodeStepGraph:
         eps = cfg.rms_norm_eps
         nat = _native
         lin = self._fused_linear
-        torch.index_select(self.embed, 0, self.token, out=self.hidden)
+        _native.embed_rows(self.embed, self.token, out=self.hidden)
         hid = self.hidden.view(-1)
         for idx, w in enumerate(self.layers):
             qkv_p, o_p = w[QKV_FUSED.removesuffix('.weight') + '._prepared'], w['self_attn.o_proj._prepared']
@@ -431,7 +468,7 @@ class DecodeStepGraph:
     def _step_unfused(self) -> None:
         cfg = self.model.config
         eps = cfg.rms_norm_eps
-        torch.index_select(self.embed, 0, self.token, out=self.hidden)
+        _native.embed_rows(self.embed, self.token, out=self.hidden)
         for idx, w in enumerate(self.layers):
             _native.add_rmsnorm(self.hidden, w['input_layernorm.weight'], eps, delta=None if idx == 0 else self.delta,
                                 out=self.states, out_sum=self.hidden)
@@ -486,31 +523,48 @@ class QuantizedQwen3ForCausalLM:
         self.rotary_emb = RotaryEmbedding(self.config.head_dim, self.config.rope_theta).to(self.device)
         self.linear_backend = linear_backend
         self.compute_stats = QuantizedComputeStats(enabled=profile_compute)
+        # (layer_idx, hidden_states) after every decoder layer, when set
+        self.layer_probe_callback = None
+        self._dequant_scratch = None
         if linear_backend is None:
             # INT8 v1 weights (``prefix.qweight`` / ``prefix.scale``).  The
             # reference dequantizes into an fp16 scratch of the largest
-            # matrix; the fused W8A16 kernel needs none, so the scratch is a
-            # zero-stride view with that element count (the capacity check of
-            # int8_weight_only_linear still applies).
-            self.dequant_scratch = torch.empty(1, device=self.device, dtype=self.dtype).expand(
-                store.max_dequant_elements)
+            # matrix; the fused W8A16 kernel needs none, so the forward passes
+            # a zero-stride view with that element count (only the capacity
+            # check of int8_weight_only_linear reads it), and the public
+            # ``dequant_scratch`` is allocated on first access.
+            self._scratch_elements = store.max_dequant_elements
+            self._forward_scratch = torch.empty(1, device=self.device, dtype=self.dtype).expand(
+                self._scratch_elements)
             from .weight_quantization.backend import CompressedLinearBackend
             self.graph_ops = CompressedLinearBackend('w8a16')
             for idx in range(self.config.num_hidden_layers):
                 _bind_int8_v1(runtime.weights_for(idx), self.graph_ops)
         else:
-            self.dequant_scratch = torch.empty(0, device=self.device, dtype=self.dtype)
+            self._scratch_elements = 0
+            self._forward_scratch = torch.empty(0, device=self.device, dtype=self.dtype)
             self.graph_ops = linear_backend
             if hasattr(linear_backend, 'fuse_projections'):
                 for idx in range(self.config.num_hidden_layers):
                     linear_backend.fuse_projections(runtime.weights_for(idx))
         self.decode_graph_enabled = decode_graph and hasattr(self.graph_ops, 'fuse_projections') and \
             self.device.type == 'cuda'
-        self._embed_device = None
+        self._embed_table = None
         self._kv_pool: dict = {}
         self.lm_head_w4 = None
         if quantize_lm_head:
             self.quantize_lm_head()
+
+    @property
+    def dequant_scratch(self) -> Tensor:
+        """The reference's persistent fp16 dequantization scratch
+        (``quantized_model.py:255-258``): the largest decoder matrix's element
+        count for INT8 v1 weights, 0 elements with a linear backend.  A real
+        contiguous buffer, allocated when first asked for (the fused kernels
+        never use it)."""
+        if self._dequant_scratch is None:
+            self._dequant_scratch = torch.empty(self._scratch_elements, device=self.device, dtype=self.dtype)
+        return self._dequant_scratch
 
     def quantize_lm_head(self, group_size: int = 128) -> None:
         """Optional W4 LM head (not in the reference, whose AWQ recipe keeps
@@ -531,10 +585,22 @@ class QuantizedQwen3ForCausalLM:
         self.lm_head_w4 = PreparedW4(tiles, meta, workspace, hidden, vocab, group_size)
         self._kv_pool = {}
 
-    def device_embedding(self) -> Tensor:
-        if self._embed_device is None:
-            self._embed_device = self.store.embed_tokens.to(self.device)
-        return self._embed_device
+    def embedding_table(self):
+        """The embedding table the decode graph gathers its token's row from.
+        The reference keeps it in host memory and embeds on the CPU
+        (``quantized_model.py:289-291``); here a CPU table stays there too, in
+        pinned memory (the store's table is replaced by its pinned copy when
+        it was not pinned), and the graph's ``wq_embed_rows`` reads the one
+        row over the host link, so the 151936 x 5120 table takes no HBM.  A
+        table already on the GPU is used in place."""
+        if self._embed_table is None:
+            table = self.store.embed_tokens
+            if table.device.type == 'cpu':
+                self._embed_table = _native.host_table(table.half(), self.device)
+                self.store.embed_tokens = self._embed_table.tensor
+            else:
+                self._embed_table = table.to(self.device, torch.float16).contiguous()
+        return self._embed_table
 
     def make_resident_cache(self, *, batch_size: int, max_seq_len: int,
                             device: str | torch.device | None = None) -> ResidentKVCache:
@@ -565,7 +631,10 @@ class QuantizedQwen3ForCausalLM:
     def __call__(self, input_ids: Tensor, *, cache: KVCache | None = None, position_ids: Tensor | None = None,
                  logits_to_keep: int = 0, **_: object) -> CausalLMOutput:
         graph = getattr(cache, '_decode_graph', None)
-        if graph is not None and position_ids is None and input_ids.shape == (1, 1):
+        # The captured step exposes no per-layer hidden state, so a probe
+        # callback sends the token through the eager layers, which call it.
+        if graph is not None and position_ids is None and input_ids.shape == (1, 1) and \
+                self.layer_probe_callback is None:
             past = cache.get_seq_length(0)
             if any(n != past for n in cache.lengths):
                 raise RuntimeError('decode graph needs every layer of the cache at the same length')
@@ -583,14 +652,27 @@ class QuantizedQwen3ForCausalLM:
             position_ids = torch.arange(past_length, past_length + query_length,
                                         device=self.device).expand(input_ids.shape[0], -1)
         cos, sin = self.rotary_emb(hidden_states, position_ids)
+        # The cache's lifecycle hooks and the per-layer probe, called where
+        # the reference calls them (``quantized_model.py:302-327``).
+        hook = lambda name: getattr(cache, name, None) if cache is not None else None  # noqa: E731
+        if (begin := hook('begin_forward')) is not None:
+            begin(query_length=query_length)
         self.runtime.begin_forward()
         for layer_idx in range(self.config.num_hidden_layers):
+            if (before := hook('before_layer')) is not None:
+                before(layer_idx)
             weights = self.runtime.weights_for(layer_idx)
             hidden_states = quantized_decoder_layer_forward(
-                hidden_states, weights, self.config, layer_idx, cos, sin, self.dequant_scratch, cache=cache,
+                hidden_states, weights, self.config, layer_idx, cos, sin, self._forward_scratch, cache=cache,
                 stats=self.compute_stats, linear_backend=self.linear_backend)
+            if self.layer_probe_callback is not None:
+                self.layer_probe_callback(layer_idx, hidden_states)
+            if (after := hook('after_layer')) is not None:
+                after(layer_idx)
             self.runtime.after_layer(layer_idx)
         self.runtime.end_forward()
+        if (end := hook('end_forward')) is not None:
+            end()
         # The norm is per row, so keeping the last rows first gives the same
         # logits as the reference's norm-then-slice without normalizing the
         # whole prompt.

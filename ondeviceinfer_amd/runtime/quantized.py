@@ -25,6 +25,8 @@ from typing import Any
 import torch
 from torch import Tensor
 
+from .stats import RuntimeStats
+
 LINEAR_WEIGHT_NAMES = (
     'self_attn.q_proj.weight',
     'self_attn.k_proj.weight',
@@ -71,13 +73,16 @@ def quantized_layer_bytes(layer: dict[str, Tensor]) -> int:
 
 
 def layer_shapes(config) -> tuple[dict[str, tuple[int, ...]], dict[str, tuple[int, int]]]:
-    """(norm name -> shape, linear weight name -> (n, k)) of one decoder layer."""
+    """(norm name -> shape, linear weight name -> (n, k)) of one decoder layer.
+    q_proj and o_proj are ``(hidden, hidden)``, as the reference's
+    ``_validate_layer`` requires (``runtime/quantized.py:135-143``);
+    ``Qwen3Config.validate`` makes ``heads * head_dim == hidden`` anyway."""
     hidden, inter, d = config.hidden_size, config.intermediate_size, config.head_dim
-    q, kv = config.num_attention_heads * d, config.num_key_value_heads * d
+    kv = config.num_key_value_heads * d
     norms = {'input_layernorm.weight': (hidden,), 'post_attention_layernorm.weight': (hidden,),
              'self_attn.q_norm.weight': (d,), 'self_attn.k_norm.weight': (d,)}
-    linears = {'self_attn.q_proj.weight': (q, hidden), 'self_attn.k_proj.weight': (kv, hidden),
-               'self_attn.v_proj.weight': (kv, hidden), 'self_attn.o_proj.weight': (hidden, q),
+    linears = {'self_attn.q_proj.weight': (hidden, hidden), 'self_attn.k_proj.weight': (kv, hidden),
+               'self_attn.v_proj.weight': (kv, hidden), 'self_attn.o_proj.weight': (hidden, hidden),
                'mlp.gate_proj.weight': (inter, hidden), 'mlp.up_proj.weight': (inter, hidden),
                'mlp.down_proj.weight': (hidden, inter)}
     return norms, linears
@@ -252,8 +257,13 @@ class QuantizedResidentRuntime:
         self.store = store
         self.device = torch.device(device)
         self.gpu_layer_budget = self.resident_count = store.config.num_hidden_layers
+        self.stats = RuntimeStats()
         self.resident = [{name: t.to(self.device) for name, t in layer.items()} for layer in store.layers]
-        self.startup_h2d_bytes = sum(quantized_layer_bytes(layer) for layer in self.resident)
+        self.stats.startup_h2d_bytes = sum(quantized_layer_bytes(layer) for layer in self.resident)
+
+    @property
+    def startup_h2d_bytes(self) -> int:
+        return self.stats.startup_h2d_bytes
 
     def begin_forward(self) -> None:
         pass

@@ -39,6 +39,7 @@ from .. import _native
 from ..config import Qwen3Config
 from ..profiling import nvtx_range
 from ..runtime.quantized import LINEAR_WEIGHT_NAMES, NORM_WEIGHT_NAMES
+from ..runtime.stats import RuntimeStats
 
 BACKEND_NAMES = ('marlin', 'int8_gemm', 'w8a16', 'reference_int4', 'reference_w8a8')
 FUSED_BACKENDS = ('marlin', 'int8_gemm', 'w8a16')
@@ -149,6 +150,20 @@ class NativeOps:
         return _native.w8a8_quantize(x)
 
     @staticmethod
+    def scaled_int8_quant(x: torch.Tensor, scale: torch.Tensor | None = None, azp: torch.Tensor | None = None,
+                          symmetric: bool = True) -> tuple[torch.Tensor, torch.Tensor, None]:
+        """vLLM's ``ops.scaled_int8_quant`` surface as the reference's kernel
+        harness calls it (``benchmarks/validate_weight_quant_kernels.py:51``):
+        dynamic per-token symmetric INT8 of a 2-D fp16 ``x``, returning
+        ``(qx int8 [M, K], scale fp32 [M, 1], None)`` from ``wq_w8a8_quantize``.
+        Static scales and asymmetric (zero-point) quantization are not part of
+        this path and raise ``ValueError``."""
+        if scale is not None or azp is not None or not symmetric:
+            raise ValueError('scaled_int8_quant: only dynamic per-token symmetric quantization is supported')
+        qx, x_scale = _native.w8a8_quantize(x)
+        return qx, x_scale.view(-1, 1), None
+
+    @staticmethod
     def w8a8_linear(qx: torch.Tensor, x_scale: torch.Tensor, prepared: PreparedW8A8,
                     output: torch.Tensor | None = None) -> torch.Tensor:
         return _native.w8a8_linear(qx, x_scale, prepared.qweight, prepared.scale, out=output)
@@ -255,8 +270,9 @@ class CompressedResidentRuntime:
     def __init__(self, store: CompressedStore, backend: 'CompressedLinearBackend', device='cuda:0',
                  verbose: bool = True):
         self.store, self.backend = store, backend
-        self.startup_h2d_bytes = sum(v.numel() * v.element_size() for layer in store.layers
-                                     for v in layer.values() if isinstance(v, torch.Tensor))
+        self.stats = RuntimeStats()
+        self.stats.startup_h2d_bytes = sum(v.numel() * v.element_size() for layer in store.layers
+                                           for v in layer.values() if isinstance(v, torch.Tensor))
         self.gpu_layer_budget = len(store.layers)
         self.resident = []
         for idx, source in enumerate(store.layers):
@@ -267,6 +283,10 @@ class CompressedResidentRuntime:
             self.resident.append(layer)
             if verbose:
                 print(f'prepared layer {idx + 1}/{len(store.layers)} for {backend.name}', flush=True)
+
+    @property
+    def startup_h2d_bytes(self) -> int:
+        return self.stats.startup_h2d_bytes
 
     @property
     def resident_storage_bytes(self) -> int:

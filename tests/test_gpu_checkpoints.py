@@ -64,6 +64,19 @@ def _run_model(model, oracle_model, gpu, tag):
         ref = qwen3.forward(token.cpu().numpy().reshape(-1), oracle_model, Cfg, ocache, logits_to_keep=1)
         _parity(out.logits[0].float().cpu().numpy(), ref, f'{tag} decode {step}')
         token = out.next_token
+    # With a layer probe set, a decode token on the graph-bound cache runs the
+    # eager layers, which call the probe after each layer
+    # (quantized_model.py:323-324 of the reference); same logits bar.
+    seen = []
+    model.layer_probe_callback = lambda idx, hidden: seen.append((idx, tuple(hidden.shape)))
+    try:
+        out = model(token, cache=cache, logits_to_keep=1)
+    finally:
+        model.layer_probe_callback = None
+    assert out.next_token is None      # not the graph's output
+    assert seen == [(i, (1, 1, Cfg.hidden_size)) for i in range(Cfg.num_hidden_layers)]
+    ref = qwen3.forward(token.cpu().numpy().reshape(-1), oracle_model, Cfg, ocache, logits_to_keep=1)
+    _parity(out.logits[0].float().cpu().numpy(), ref, f'{tag} probed decode')
 
 
 def _oracle_globals(path_global):
@@ -101,16 +114,31 @@ def test_pack_quantized_checkpoint_from_disk(gpu, tmp_path):
 
 
 def test_int8_v1_checkpoint_from_disk(gpu, tmp_path):
-    from ondeviceinfer_amd.quantized_model import QuantizedQwen3ForCausalLM, int8_weight_only_linear
+    from ondeviceinfer_amd.quantized_model import (QuantizedQwen3ForCausalLM, TiledInt8QWeight,
+                                                   int8_weight_only_linear)
     from ondeviceinfer_amd.runtime.quantized import (QuantizedResidentRuntime, load_quantized_cpu_weight_store,
-                                                     qweight_name, scale_name, write_int8_checkpoint)
+                                                     qweight_name, scale_name, validate_int8_layer,
+                                                     write_int8_checkpoint)
     from ondeviceinfer_amd.weight_quantization.synthetic import random_int8_store
     path = write_int8_checkpoint(tmp_path / 'int8', random_int8_store(_qcfg(), seed=2, device=gpu))
     np_layers = [load_np(str(path / f'layer-{i:03d}.safetensors')) for i in range(Cfg.num_hidden_layers)]
     store = load_quantized_cpu_weight_store(path, pin_memory=True, progress=False, verify_checksums=True)
     assert store.all_pinned
     runtime = QuantizedResidentRuntime(store, device=gpu)
+    assert runtime.stats.startup_h2d_bytes == store.decoder_bytes
     model = QuantizedQwen3ForCausalLM(store, runtime, device=gpu, linear_backend=None)
+    # The bound model holds each weight once, as INT8 tiles; the reference's
+    # keys stay, still pass the loader's per-layer checks and read back as the
+    # checkpoint's row-major INT8 bit for bit.
+    for idx, layer in enumerate(runtime.resident):
+        validate_int8_layer({k: v for k, v in layer.items() if not k.endswith('._prepared')}, idx, store.config)
+        for name in qwen3.LINEAR_NAMES:
+            q = layer[qweight_name(name)]
+            assert isinstance(q, TiledInt8QWeight) and q.dtype == torch.int8
+            assert np.array_equal(q.cpu().numpy(), np_layers[idx][qweight_name(name)])
+            assert np.array_equal(layer[scale_name(name)].cpu().numpy(), np_layers[idx][scale_name(name)])
+    assert model.dequant_scratch.is_contiguous()
+    assert model.dequant_scratch.numel() == store.max_dequant_elements
     rng = np.random.default_rng(4)
     linears = []
     for idx, layer in enumerate(runtime.resident):

@@ -254,6 +254,56 @@ def test_decode_attention_graph_replays_follow_the_position(nat):
         _ = torch.randn(1000, device='cuda').sum().item()   # eager work between replays
 
 
+@pytest.mark.parametrize('on_host', [True, False])
+def test_embed_rows(nat, on_host):
+    """wq_embed_rows gathers the rows of device token ids bit-exactly from a
+    table in pinned host memory (the decode graph's embedding) or on the
+    device; an out-of-range id gives a NaN row."""
+    print(f'[embed_rows] on_host={on_host}', flush=True)
+    vocab, hidden = 1000, 5120
+    table = (torch.randn(vocab, hidden, generator=torch.Generator().manual_seed(1)) * 0.02).half()
+    src = nat.host_table(table, 'cuda:0') if on_host else table.cuda()
+    if on_host:
+        assert src.tensor.is_pinned() and torch.equal(src.tensor, table)
+    ids = torch.tensor([0, 999, 17, 17, 523], dtype=torch.long, device='cuda')
+    out = nat.embed_rows(src, ids)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), table[ids.cpu()])
+    bad = nat.embed_rows(src, torch.tensor([3, -1, 1000], dtype=torch.long, device='cuda'))
+    torch.cuda.synchronize()
+    bad = bad.cpu()
+    assert torch.equal(bad[0], table[3]) and bool(torch.isnan(bad[1:]).all())
+    with pytest.raises(ValueError):
+        nat.host_table(table.cuda(), 'cuda:0')
+
+
+@pytest.mark.parametrize('count', [1, 2, 3, 5, 7, 320, 512])
+def test_rmsnorm_prologue_any_sumsq_count(nat, count):
+    """The RMSNorm prologue sums however many partial sums of squares the
+    producer left (0 < count <= 512), including counts below one float4 and
+    counts that are not a multiple of 4; the output is the oracle's norm."""
+    from oracle import synth
+    k, n = 5120, 1024
+    print(f'[rmsnorm_prologue] count={count}', flush=True)
+    w, _ = synth.w4_case(n, k, 1, seed=count)
+    rng = np.random.default_rng(count)
+    key = 'mlp.up_proj'
+    tiles, meta = nat.w4_repack(torch.from_numpy(w[f'{key}.weight_packed']).cuda(),
+                                torch.from_numpy(w[f'{key}.weight_scale']).cuda(),
+                                torch.from_numpy(w[f'{key}.weight_zero_point']).cuda(), n, k, 128)
+    xin = (rng.standard_normal(k) * 3).astype(np.float16)
+    nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float16)
+    sq = xin.astype(np.float32) ** 2
+    parts = np.array([c.sum(dtype=np.float64) for c in np.array_split(sq, count)], dtype=np.float32)
+    out = nat.w4a16_decode_fused(torch.from_numpy(xin).cuda(), tiles, meta, n, 128, x_mode=nat.X_RMSNORM,
+                                 norm_weight=torch.from_numpy(nw).cuda(), sumsq_in=torch.from_numpy(parts).cuda(),
+                                 eps=1e-6)
+    torch.cuda.synchronize()
+    expect = qdq.qdq_linear(qwen3.rms_norm(xin, nw, 1e-6)[None], w, f'{key}.weight')[0]
+    m = qdq.parity_metrics(out.cpu().numpy().astype(np.float32), expect.astype(np.float32))
+    assert qdq.parity_ok(m), m
+
+
 @pytest.mark.parametrize('k,n,mode', [(5120, 7168, 1), (5120, 5120, 0), (17408, 5120, 2), (5120, 34816, 1),
                                       (512, 1024, 2)])
 def test_w4a16_decode_fused_matches_oracle(nat, k, n, mode):

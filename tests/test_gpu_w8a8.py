@@ -43,6 +43,17 @@ def test_w8a8_quantize_bit_exact(m, k, scale):
     assert np.array_equal(host(sx), s_ref)
 
 
+def test_scaled_int8_quant_harness_surface():
+    """``backend.ops.scaled_int8_quant(x)`` as the reference's kernel harness
+    calls it (``validate_weight_quant_kernels.py:51``): ``(qx, scale [M, 1],
+    None)``, bit-exact against the oracle's per-token quantizer."""
+    x = (np.random.default_rng(11).standard_normal((32, 5120)) * 0.1).astype(np.float16)
+    qx, sx, azp = wq.CompressedLinearBackend('int8_gemm').ops.scaled_int8_quant(dev(x))
+    q_ref, s_ref = qdq.quantize_activations_per_token(x)
+    assert azp is None and qx.dtype == torch.int8 and tuple(sx.shape) == (32, 1) and sx.dtype == torch.float32
+    assert np.array_equal(host(qx), q_ref) and np.array_equal(host(sx).reshape(-1), s_ref)
+
+
 @pytest.mark.parametrize('m,n,k,with_bias', [
     (1, 5120, 5120, False),      # decode, q/o shape
     (1, 1024, 17408, True),      # decode, long k
