@@ -120,7 +120,10 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
  * Every call on a GPU shares that GPU's array: calls that may overlap on one
  * GPU (different streams, or graphs replayed concurrently) race and must be
  * ordered by the caller.  The first call on a device looks the array up
- * (hipGetSymbolAddress) and queues a clear of it on `stream`.  Shapes whose
+ * (hipGetSymbolAddress) and queues a clear of it on `stream`; that first call
+ * must not be under stream capture (it returns WQ_ERR_UNSUPPORTED there, so
+ * no clear is ever recorded into a graph): make one eager call per device
+ * before capturing later ones, which then record only the linear.  Shapes whose
  * split plan would need more than 4 MiB return WQ_ERR_WORKSPACE (none of the
  * planner's current shapes do: its largest split needs 2 MiB).
  * No counterpart in the reference: it exists for callers that cannot

@@ -345,7 +345,11 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint4_t* p, size_t n16)
 // Device address of `scratch` on the current device.  The first call on a
 // device looks the address up and queues a clear of the whole array on
 // `stream` (the split counters must start at zero; every later call leaves
-// them at zero again), ahead of the caller's kernels on that stream.
+// them at zero again), ahead of the caller's kernels on that stream.  That
+// set-up is refused while `stream` is being captured: the clear would be
+// recorded into the caller's graph and rerun on every replay, and eager calls
+// before the first replay would find the counters uncleared.  One eager call
+// on the device, before capture, does the set-up.
 int noalloc_scratch(hipStream_t stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -357,6 +361,15 @@ int noalloc_scratch(hipStream_t stream, void** out) {
              dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &capture);
+    if (e != hipSuccess) {
+      set_error("hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+      return WQ_ERR_HIP;
+    }
+    WQ_REQUIRE(capture == hipStreamCaptureStatusNone, WQ_ERR_UNSUPPORTED,
+               "wq_w4a16_linear_noalloc: the first call on device %d sets up its scratch and must not be captured; "
+               "make one call outside graph capture first", dev);
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || ptr == nullptr) {

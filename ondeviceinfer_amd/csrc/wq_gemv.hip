@@ -850,10 +850,20 @@ struct FlatPlan {
 // register count and leaves a second launch wave.  Otherwise one workgroup
 // per tile: 12 waves for N < 1024 tiles (enough loads in flight), 4 for wide
 // N.
+constexpr int kFlatSplitMaxTiles = 512;   // only shapes with fewer tiles split their k range
+
+// Split workspace layout: one uint32 arrival counter per tile in a fixed
+// region sized for the largest split shape, then the fp32 partials.  The
+// counter region does not depend on the shape, so one buffer shared by
+// several shapes (the allocation-free entry point's scratch) never has one
+// shape's partials written over another shape's counters.
+constexpr size_t kFlatCounterBytes = 4 * kFlatSplitMaxTiles;
+static_assert(kFlatCounterBytes % 256 == 0, "partials start 256-byte aligned");
+
 template <WFmt F>
 FlatPlan plan_flat(int ntile, int nblk, bool may_split = true) {
   FlatPlan p{1, 1};
-  if (ntile < 512 && nblk >= 64) p.split = 4;
+  if (ntile < kFlatSplitMaxTiles && nblk >= 64) p.split = 4;
   if (p.split > nblk || !may_split) p.split = 1;
   const int per = nblk / p.split;
   int ksw = p.split > 1 || ntile >= 1024 ? 4 : 12;
@@ -866,7 +876,7 @@ FlatPlan plan_flat(int ntile, int nblk, bool may_split = true) {
 
 size_t flat_workspace_bytes(int ntile, int split) {
   if (split <= 1) return 0;
-  return (((size_t)ntile * 4 + 255) & ~(size_t)255) + (size_t)ntile * split * 64 * sizeof(float4_t);
+  return kFlatCounterBytes + (size_t)ntile * split * 64 * sizeof(float4_t);
 }
 
 template <int NB, int MM, WFmt F, XMode XM>
@@ -877,8 +887,7 @@ int launch_flat(const half_t* x, int M, int K, const void* w, const void* meta, 
   if (lds > kGemvMaxBytes) return kNotApplicable;
   const int ntile = (N + 15) / 16;
   uint32_t* cnt = reinterpret_cast<uint32_t*>(ws);
-  float4_t* part = p.split > 1 ? reinterpret_cast<float4_t*>(reinterpret_cast<uint8_t*>(ws) +
-                                                             (((size_t)ntile * 4 + 255) & ~(size_t)255))
+  float4_t* part = p.split > 1 ? reinterpret_cast<float4_t*>(reinterpret_cast<uint8_t*>(ws) + kFlatCounterBytes)
                                : nullptr;
   hipLaunchKernelGGL((gemv_flat_kernel<NB, MM, F, XM>), dim3((unsigned)ntile, (unsigned)p.split), dim3(64 * p.ksw),
                      lds, s, x, M, K, w, meta, bias, N, fmt_arg, y, p.split, part, cnt, fz);

@@ -71,3 +71,40 @@ def test_noalloc_rejects_bad_shapes_on_the_host(gpu):
     assert rc != 0 and b'group' in lib.wq_last_error()
     rc = lib.wq_w4a16_linear_noalloc(None, 1, 256, None, None, 16, 128, None, None)
     assert rc == _native.WQ_ERR_INVALID_ARGUMENT
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """After one eager call on the device (the scratch set-up), calls captured
+    in a HIP graph record only the linear: several replays on the k-split
+    shapes, with eager work and synchronizations between them, each equal bit
+    for bit to wq_w4a16_linear with a caller workspace."""
+    gen = torch.Generator(device=gpu).manual_seed(1)
+    shapes = [(5120, 17408), (1024, 8448)]
+    preps = [_prepared(n, k, 10 + i, gpu) for i, (n, k) in enumerate(shapes)]
+    xs = [torch.randn(1, k, generator=gen, device=gpu).half() for _, k in shapes]
+    ys = [torch.empty(1, n, dtype=torch.float16, device=gpu) for n, _ in shapes]
+    lib = _native.load()
+    _noalloc(xs[0], preps[0], shapes[0][0])          # eager set-up call (already done if earlier tests ran)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for (n, k), p, x, y in zip(shapes, preps, xs, ys):
+                rc = lib.wq_w4a16_linear_noalloc(x.data_ptr(), 1, k, p.tiles.data_ptr(), p.meta.data_ptr(), n, 128,
+                                                 y.data_ptr(), stream.cuda_stream)
+                assert rc == 0, lib.wq_last_error()
+    for rep in range(4):
+        print(f'noalloc graph replay {rep}', flush=True)
+        for x in xs:                                   # new inputs, written eagerly between replays
+            x.copy_(torch.randn(x.shape, generator=gen, device=gpu).half())
+        for y in ys:
+            y.fill_(float('nan'))
+        graph.replay()
+        torch.cuda.synchronize()
+        for (n, k), p, x, y in zip(shapes, preps, xs, ys):
+            expected, _ = _with_workspace(x, p, n)
+            torch.cuda.synchronize()
+            assert torch.equal(y, expected), f'replay {rep} n={n} k={k}'
+        # an eager noalloc call between replays shares the same scratch
+        assert torch.equal(_noalloc(xs[1], preps[1], shapes[1][0]), _with_workspace(xs[1], preps[1], shapes[1][0])[0])
