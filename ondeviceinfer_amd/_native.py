@@ -31,7 +31,7 @@ WQ_ERR_WORKSPACE = 4
 ABI_VERSION = 1
 
 W4_BLOCK_K = 128
-DECODE_ATTENTION_MAX_SEQ = 16384   # wq_decode_attention: 64 workgroups x 4 sub-chunks x 64 positions per kv head
+DECODE_ATTENTION_MAX_SEQ = 16384   # wq_decode_attention: the largest cache (max_seq) it takes
 W4_META_BYTES = 40
 W8_BLOCK_K = 128
 

@@ -20,10 +20,10 @@ namespace {
 constexpr int kHeadDim = 128;     // Qwen3 head_dim; one lane holds two elements
 constexpr int kBlock = 16;        // KV positions per attention block (one wave's matrix tile)
 constexpr int kMaxGroup = 8;      // q heads per kv head
-constexpr int kSub = 4 * kBlock;  // KV positions per attention sub-chunk (one block per wave)
-constexpr int kMaxChunks = 64;    // attention workgroups per kv head (one merge thread each)
-constexpr int kMaxSpc = 4;        // sub-chunks per workgroup
-constexpr int kMaxSeq = kMaxChunks * kMaxSpc * kSub;
+constexpr int kMaxBlocksPerWave = 4;
+constexpr int kMaxChunks = 64;    // attention workgroups per kv head (one merge lane each)
+constexpr int kMaxSeq = 16384;    // positions of the cache (the API's limit)
+static_assert(kMaxSeq <= kMaxChunks * 4 * kMaxBlocksPerWave * kBlock, "the four-wave split covers the largest cache");
 
 
 // ------------------------------------------------------------------ RMSNorm
@@ -105,22 +105,39 @@ __device__ __forceinline__ half2_t norm_rope_pair(half2_t v, bool norm, half2_t 
   return t1 + t2;
 }
 
-// Work split of the attention: a kv head's positions go to `nc` workgroups
-// of `spc` (1 .. 4) consecutive sub-chunks of 64 positions, spc the fewest
-// that keep nc <= kMaxChunks (the merge reads one partial per workgroup).
-// Within a sub-chunk wave w takes the block of positions 16w .. 16w + 15.
-// Measured against other splits of the same cache on MI355X (fixed grids of
-// 256 - 1024 workgroups with blocks dealt round-robin, or fewer, longer
-// chunks), this one, about one workgroup per compute unit at 4K positions
-// and 8 kv heads, streams fastest and keeps the merge short.
+// Work split of the attention: a kv head's cache is cut into `nc` chunks of
+// `nbc` 16-position blocks, one workgroup of `sw` waves each; wave w takes
+// blocks w, w + sw, ...  Five waves when about one workgroup per compute unit
+// over the whole grid (256 / kv_heads chunks per kv head) leaves each wave
+// at most two blocks, the chunk rounded up to whole rounds of the five waves:
+// at the Qwen3-14B geometry with a 4229-position cache, 27 chunks of 10
+// blocks per kv head, 216 workgroups.  Longer caches take four-wave
+// workgroups of 4, 8, 12 or 16 blocks, as few as keep nc <= 64 (at 16384
+// positions 64 chunks of 16 blocks, two workgroups per compute unit; five
+// waves of four blocks need 174 registers, one workgroup per unit).
+// Measured on MI355X (40 layers, 4229 positions, position 4101): 7.4 us for
+// the attention launch against 7.9 for four-wave workgroups of 8 blocks (272
+// workgroups, 16 of them sharing a compute unit), 8.6 for four waves of 9
+// blocks (the third block of wave 0 costs more than the shared units did),
+// 7.7 for six waves of 12, 8.8 for eight of 16.  With 8 kv heads the chunks
+// of kv head h are workgroups h, h + 8, ..., all on XCD h.
 struct AttnSplit {
-  int spc, nc;
+  int nbc, nc, bpw, sw;   // blocks per chunk, chunks per kv head, blocks per wave, waves per workgroup
 };
 
-AttnSplit attn_split(int64_t max_seq) {
-  const int64_t subs = (max_seq + kSub - 1) / kSub;
-  const int64_t spc = (subs + kMaxChunks - 1) / kMaxChunks;
-  return {(int)spc, (int)((subs + spc - 1) / spc)};
+AttnSplit attn_split(int64_t kv_heads, int64_t max_seq) {
+  const int64_t blocks = (max_seq + kBlock - 1) / kBlock;
+  int64_t target = 256 / kv_heads;
+  target = target < 1 ? 1 : (target > kMaxChunks ? kMaxChunks : target);
+  int64_t nbc = ((blocks + target - 1) / target + 4) / 5 * 5;
+  int sw = 5;
+  if (nbc > 2 * 5) {
+    sw = 4;
+    const int64_t subs = (blocks + 3) / 4;                     // four-block sub-chunks
+    nbc = 4 * ((subs + kMaxChunks - 1) / kMaxChunks);
+  }
+  const int64_t nc = (blocks + nbc - 1) / nbc;
+  return {(int)nbc, (int)nc, (int)((nbc + sw - 1) / sw), sw};
 }
 
 // Orders this wave's LDS accesses around a wave-private exchange (the
@@ -133,16 +150,22 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// grid = (kv_heads, nc); 256 threads = 4 waves.  Workgroup c of kv head h
-// covers positions [c * SPC * 64, (c + 1) * SPC * 64); in each sub-chunk
-// wave w owns the block 16w .. 16w + 15 and runs its own online softmax over
-// its blocks for the head's G <= 8 query heads, so the block loop has no
-// workgroup barrier.  Lane l is (r, i) = (l / 16, l % 16).
-//   loads   the prologue's operands (q, cos/sin rows, norm weights, the new
-//           k/v) are requested first, then every K fragment and V row of the
-//           wave's blocks (rows clamped into the cache; rows past L or at
-//           `pos` are replaced below), so the q/k prologue runs while the
-//           cache streams in;
+// grid = kv_heads * nc workgroups (flat id f: kv head f % kv_heads, chunk
+// f / kv_heads); SW = 5 or 4 waves.  Chunk c covers positions
+// [c * nbc * 16, (c + 1) * nbc * 16); wave w owns blocks w, w + SW, ... (16
+// positions each, BPW at most) and runs its own online softmax over them for
+// the head's G <= 8 query heads, so the block loop has no workgroup barrier.
+// Lane l is (r, i) = (l / 16, l % 16).
+//   loads   the position, then the prologue's operands (q heads w and w + SW,
+//           cos/sin rows, norm weights, the new k/v), then every K fragment
+//           and V row of the wave's blocks (rows clamped into the cache; rows
+//           past L or at `pos` are replaced below), so the q/k prologue runs
+//           while the
+//           cache streams in (issuing the stream itself takes the wave about
+//           1.5 us: the memory pipeline accepts the requests only as fast as
+//           it drains them);
+//   prologue q/k RMSNorm + RoPE, q and (in the chunk that holds `pos`) the
+//           new key / value to LDS, the new key / value appended to the cache;
 //   scores  S[g][p] = q_g . k_p on the matrix cores (16x16x32): A = the query
 //           heads (rows g, zero past G), B = the block's 16 key rows (each
 //           lane 16 bytes of one row); lane (r, i) gets heads 4r .. 4r+3 at
@@ -153,68 +176,55 @@ __device__ __forceinline__ void wave_lds_sync() {
 //           arrive 16 bytes of d per lane and are written transposed), one
 //           MFMA per 16 values of d; the accumulator rows are the heads 4r+v
 //           of the lane's own softmax row, so the online rescale is local.
-// At the end the four waves' (max, sum, output) are combined through LDS.
-// The workgroup that holds `pos` also normalizes, rotates and appends the
-// new key and value, and takes them from LDS.  With one
-// workgroup per head it writes the output; otherwise every workgroup, active
-// or not, writes its (max, sum) pair and unnormalized output to the
-// workspace, and decode_attention_merge_kernel (the next launch) combines
-// them without reading the position: an empty workgroup writes (-inf, 0) and
-// zeros and weighs nothing, and an invalid position leaves every max at
-// -inf, which the merge turns into NaN.
-template <int G, int SPC>
-__global__ __launch_bounds__(256, 2) void decode_attention_kernel(
+// The waves' (max, sum, output) are combined through LDS.  Rows past L
+// and row `pos` (fetched before it was written) are replaced: P = 0 and
+// zeroed V past L, the LDS copies at `pos`.  With one workgroup per head the
+// workgroup writes the output; otherwise every workgroup, active or not,
+// writes its (max, sum) pair and unnormalized output to the workspace, and
+// decode_attention_merge_kernel (the next launch) combines them without
+// reading the position: an empty chunk writes (-inf, 0) and zeros and
+// weighs nothing, and an invalid position leaves every max at -inf, which
+// the merge turns into NaN.
+template <int G, int BPW, int SW>
+__global__ __launch_bounds__(64 * SW, 2) void decode_attention_kernel(
     const half_t* __restrict__ qkv, int H, int KV, const half_t* __restrict__ qn_w,
     const half_t* __restrict__ kn_w, float eps, const half_t* __restrict__ cos_t, const half_t* __restrict__ sin_t,
-    const int32_t* __restrict__ position, half_t* kc, half_t* vc, int max_seq, float scale_log2,
+    const int32_t* __restrict__ position, half_t* kc, half_t* vc, int max_seq, float scale_log2, int nbc,
     half_t* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   constexpr int D = kHeadDim, GM = kMaxGroup;
   constexpr int VTS = 20;   // V^T row stride in halves (40 bytes: the 16 B-fragment reads hit distinct banks)
   __shared__ __attribute__((aligned(16))) half_t qh[GM][D];
   __shared__ __attribute__((aligned(16))) half_t knew[D];
   __shared__ __attribute__((aligned(16))) half_t vnew[D];
-  __shared__ __attribute__((aligned(16))) half_t pl[4][16][16];    // per-wave P, [head][position]
-  __shared__ __attribute__((aligned(16))) half_t vt[4][D][VTS];    // per-wave V^T, [d][position]
-  __shared__ __attribute__((aligned(16))) float red[4][GM][D];    // per-wave unnormalized outputs
-  __shared__ float mlw[4][GM][2];                                 // per-wave (max, sum)
+  __shared__ __attribute__((aligned(16))) half_t pl[SW][16][16];    // per-wave P, [head][position]
+  __shared__ __attribute__((aligned(16))) half_t vt[SW][D][VTS];    // per-wave V^T, [d][position]
+  __shared__ __attribute__((aligned(16))) float red[SW][GM][D];    // per-wave unnormalized outputs
+  __shared__ float mlw[SW][GM][2];                                 // per-wave (max, sum)
 
-  const int h = blockIdx.x, chunk = blockIdx.y, NC = gridDim.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x % KV, chunk = blockIdx.x / KV, NC = gridDim.x / KV;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 15, kb = lane >> 4;
-  const int pos = *position;
-  const bool valid = pos >= 0 && pos < max_seq;
-  const int L = valid ? pos + 1 : 0;
-  const int p0 = chunk * SPC * kSub;
-  if (p0 >= L) {
-    // Nothing to attend in this chunk (in any chunk when the position is
-    // invalid; chunk 0 is active whenever it is valid).
-    if (NC == 1) {
-      for (int j = tid; j < G * D; j += 256) out[(size_t)h * G * D + j] = (half_t)__builtin_nanf("");
-    } else {
-      for (int j = tid; j < G * (D / 4); j += 256) {
-        const size_t slot = (size_t)(h * G + j / (D / 4)) * NC + chunk;
-        *reinterpret_cast<float4_t*>(ws_o + slot * D + 4 * (j % (D / 4))) = float4_t{0.f, 0.f, 0.f, 0.f};
-      }
-      if (tid < G) {
-        ws_ml[((size_t)(h * G + tid) * NC + chunk) * 2] = -INFINITY;
-        ws_ml[((size_t)(h * G + tid) * NC + chunk) * 2 + 1] = 0.f;
-      }
-    }
-    return;
-  }
-  const bool owner = pos >= p0 && pos < p0 + SPC * kSub;
+  const int p0 = chunk * nbc * kBlock;
   const half_t* kh = kc + (size_t)h * max_seq * D;
   const half_t* vh = vc + (size_t)h * max_seq * D;
   const int dg = lane & 15, q4 = lane >> 4;   // V rows: elements 8dg.., the block's positions 4q4 .. 4q4+3
 
-  // 1) The prologue's operands: query heads wave and wave + 4, the new
-  //    key (owner wave 0) or value (owner wave 1), norm weights, cos / sin.
-  const half2_t c2 = reinterpret_cast<const half2_t*>(cos_t + (size_t)pos * D)[lane];
-  const half2_t s2 = reinterpret_cast<const half2_t*>(sin_t + (size_t)pos * D)[lane];
+  // 1) The position, then the prologue's operands: query heads wave and
+  //    wave + SW, the new key (owner wave 0) or value (owner wave 1), norm
+  //    weights, cos / sin at the position.
+  const int pos = *position;
+  const bool valid = pos >= 0 && pos < max_seq;
+  const int L = valid ? pos + 1 : 0;
+  const bool owner = valid && pos >= p0 && pos < p0 + nbc * kBlock;
+  const int prow = valid ? pos : 0;
+  const half2_t c2 = reinterpret_cast<const half2_t*>(cos_t + (size_t)prow * D)[lane];
+  const half2_t s2 = reinterpret_cast<const half2_t*>(sin_t + (size_t)prow * D)[lane];
+  static_assert(SW >= kMaxGroup / 2, "two query heads per wave at most");
   half2_t qv[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int g = wave + 4 * j;
+    const int g = wave + SW * j;
     qv[j] = g < G ? reinterpret_cast<const half2_t*>(qkv + (size_t)(h * G + g) * D)[lane] : half2_t{};
   }
   const half2_t nq = qn_w ? reinterpret_cast<const half2_t*>(qn_w)[lane] : half2_t{};
@@ -225,19 +235,22 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   }
   if (owner && wave == 1) nv = reinterpret_cast<const half2_t*>(qkv + (size_t)(H + KV + h) * D)[lane];
 
-  // 2) The cache stream: this wave's block of sub-chunk j starts at pb.
-  uint4_t kr[SPC][4], vr[SPC][4];
+  // 2) The cache stream: this wave's blocks w, w + SW, ... of the chunk.
+  //    Every slot issues its loads (a slot past the chunk's blocks rereads
+  //    the chunk's last block, a cache hit, and is never used), so the
+  //    prologue's wait counts only the requests issued after its own.
+  uint4_t kr[BPW][4], vr[BPW][4];
 #pragma unroll
-  for (int j = 0; j < SPC; ++j) {
-    const int pb = p0 + j * kSub + kBlock * wave;
+  for (int b = 0; b < BPW; ++b) {
+    const int pb = p0 + min(wave + SW * b, nbc - 1) * kBlock;
     const int rk = min(pb + i, max_seq - 1);
     const uint4_t* ks_src = reinterpret_cast<const uint4_t*>(kh + (size_t)rk * D + 8 * kb);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kr[j][ks] = ks_src[4 * ks];
+    for (int ks = 0; ks < 4; ++ks) kr[b][ks] = ks_src[4 * ks];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int rv = min(pb + 4 * q4 + e, max_seq - 1);
-      vr[j][e] = *reinterpret_cast<const uint4_t*>(vh + (size_t)rv * D + 8 * dg);
+      vr[b][e] = *reinterpret_cast<const uint4_t*>(vh + (size_t)rv * D + 8 * dg);
     }
   }
 
@@ -246,9 +259,9 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   //    issued before and are replaced by the LDS copies).
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int g = wave + 4 * j;
+    const int g = wave + SW * j;
     const half2_t r = g < G ? norm_rope_pair(qv[j], qn_w != nullptr, nq, eps, c2, s2, lane) : half2_t{};
-    reinterpret_cast<half2_t*>(qh[g])[lane] = r;
+    if (g < GM) reinterpret_cast<half2_t*>(qh[g])[lane] = r;
   }
   if (owner && wave == 0) {
     const half2_t r = norm_rope_pair(nv, kn_w != nullptr, nk, eps, c2, s2, lane);
@@ -260,6 +273,24 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
     reinterpret_cast<half2_t*>(vc + (size_t)h * max_seq * D + (size_t)pos * D)[lane] = nv;
   }
   __syncthreads();
+
+  if (p0 >= L) {
+    // Nothing to attend in this chunk (in any chunk when the position is
+    // invalid; chunk 0 is active whenever it is valid).
+    if (NC == 1) {
+      for (int j = tid; j < G * D; j += 64 * SW) out[(size_t)h * G * D + j] = (half_t)__builtin_nanf("");
+    } else {
+      for (int j = tid; j < G * (D / 4); j += 64 * SW) {
+        const size_t slot = (size_t)(h * G + j / (D / 4)) * NC + chunk;
+        *reinterpret_cast<float4_t*>(ws_o + slot * D + 4 * (j % (D / 4))) = float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      if (tid < G) {
+        ws_ml[((size_t)(h * G + tid) * NC + chunk) * 2] = -INFINITY;
+        ws_ml[((size_t)(h * G + tid) * NC + chunk) * 2 + 1] = 0.f;
+      }
+    }
+    return;
+  }
 
   half8_t qa[4];
 #pragma unroll
@@ -276,17 +307,17 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   }
 
 #pragma unroll
-  for (int s = 0; s < SPC; ++s) {
-    const int ps = p0 + s * kSub + kBlock * wave;   // the block's first position (wave-uniform)
-    if (ps < L) {
+  for (int b = 0; b < BPW; ++b) {
+    const int ps = p0 + (wave + SW * b) * kBlock;   // the block's first position (wave-uniform)
+    if (wave + SW * b < nbc && ps < L) {
       const int pk = ps + i;
       if (pk == pos) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kr[s][ks] = *reinterpret_cast<const uint4_t*>(knew + 32 * ks + 8 * kb);
+        for (int ks = 0; ks < 4; ++ks) kr[b][ks] = *reinterpret_cast<const uint4_t*>(knew + 32 * ks + 8 * kb);
       }
       float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) acc = mfma16(qa[ks], __builtin_bit_cast(half8_t, kr[s][ks]), acc);
+      for (int ks = 0; ks < 4; ++ks) acc = mfma16(qa[ks], __builtin_bit_cast(half8_t, kr[b][ks]), acc);
       // Position ps < L is in every row, so each row max is finite.
       float pv[4], alpha[4];
 #pragma unroll
@@ -294,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
         const float sv = pk < L ? acc[v] * scale_log2 : -INFINITY;
         const float mn = fmaxf(m_run[v], row_max16(sv));
         pv[v] = exp2_hw(sv - mn);           // -inf -> 0
-        alpha[v] = exp2_hw(m_run[v] - mn);  // 0 on the wave's first sub-chunk
+        alpha[v] = exp2_hw(m_run[v] - mn);  // 0 on the wave's first block
         l_run[v] = l_run[v] * alpha[v] + row_sum16(pv[v]);
         m_run[v] = mn;
       }
@@ -305,9 +336,9 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
       for (int e = 0; e < 4; ++e) {
         const int p = ps + 4 * q4 + e;
         v8[e] = p == pos ? *reinterpret_cast<const half8_t*>(vnew + 8 * dg)
-                         : (p < L ? __builtin_bit_cast(half8_t, vr[s][e]) : half8_t{});
+                         : (p < L ? __builtin_bit_cast(half8_t, vr[b][e]) : half8_t{});
       }
-      wave_lds_sync();   // the previous sub-chunk's fragment reads are done
+      wave_lds_sync();   // the previous block's fragment reads are done
 #pragma unroll
       for (int v = 0; v < 4; ++v) pl[wave][4 * kb + v][i] = (half_t)pv[v];
 #pragma unroll
@@ -345,17 +376,17 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(
   }
   __syncthreads();
 
-  // Combine the four waves (a wave with no position below L has max -inf,
+  // Combine the waves (a wave with no position below L has max -inf,
   // sum 0 and output 0; wave 0 always has one, so M is finite).
-  for (int j = tid; j < G * (D / 4); j += 256) {
+  for (int j = tid; j < G * (D / 4); j += 64 * SW) {
     const int g = j / (D / 4), d = 4 * (j % (D / 4));
     float M = mlw[0][g][0];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) M = fmaxf(M, mlw[w][g][0]);
+    for (int w = 1; w < SW; ++w) M = fmaxf(M, mlw[w][g][0]);
     float4_t num = {0.f, 0.f, 0.f, 0.f};
     float den = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < SW; ++w) {
       const float wt = exp2_hw(mlw[w][g][0] - M);
       num += wt * *reinterpret_cast<const float4_t*>(&red[w][g][d]);
       den += wt * mlw[w][g][1];
@@ -416,7 +447,7 @@ __global__ __launch_bounds__(128) void decode_attention_merge_kernel(int NC, con
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t attention_workspace_bytes(int64_t H, int64_t KV, int64_t max_seq) {
-  const int64_t nc = attn_split(max_seq).nc;
+  const int64_t nc = attn_split(KV, max_seq).nc;
   const int64_t g = H / KV;
   return nc <= 1 ? 0 : align256((size_t)KV * nc * g * 2 * 4) + (size_t)KV * nc * g * kHeadDim * 4;
 }
@@ -579,7 +610,7 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
              "null pointer argument");
   WQ_REQUIRE(((uintptr_t)qkv | (uintptr_t)key_cache | (uintptr_t)value_cache) % 16 == 0, WQ_ERR_INVALID_ARGUMENT,
              "qkv and the caches must be 16-byte aligned");
-  const AttnSplit split = attn_split(max_seq);
+  const AttnSplit split = attn_split(kv_heads, max_seq);
   const int64_t nc = split.nc;
   const size_t need = attention_workspace_bytes(q_heads, kv_heads, max_seq);
   WQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), WQ_ERR_WORKSPACE,
@@ -589,21 +620,26 @@ extern "C" int wq_decode_attention(const uint16_t* qkv, int64_t q_heads, int64_t
                                               align256((size_t)kv_heads * nc * (q_heads / kv_heads) * 2 * 4))
                    : nullptr;
   auto launch = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, dim3((unsigned)kv_heads, (unsigned)nc), dim3(256), 0, as_stream(stream),
+    hipLaunchKernelGGL(kernel, dim3((unsigned)(kv_heads * nc)), dim3(64 * split.sw), 0, as_stream(stream),
                        reinterpret_cast<const half_t*>(qkv), (int)q_heads, (int)kv_heads,
                        reinterpret_cast<const half_t*>(q_norm_weight), reinterpret_cast<const half_t*>(k_norm_weight),
                        eps, reinterpret_cast<const half_t*>(cos_table), reinterpret_cast<const half_t*>(sin_table),
                        position, reinterpret_cast<half_t*>(key_cache), reinterpret_cast<half_t*>(value_cache),
-                       (int)max_seq, scale * kLog2e, reinterpret_cast<half_t*>(out), po, ml);
+                       (int)max_seq, scale * kLog2e, split.nbc, reinterpret_cast<half_t*>(out), po, ml);
   };
   const int g = (int)(q_heads / kv_heads);
 #define WQ_ATTN_CASE(GG)                                                                     \
   case GG:                                                                                   \
-    switch (split.spc) {                                                                     \
-      case 1: launch(decode_attention_kernel<GG, 1>); break;                                 \
-      case 2: launch(decode_attention_kernel<GG, 2>); break;                                 \
-      case 3: launch(decode_attention_kernel<GG, 3>); break;                                 \
-      default: launch(decode_attention_kernel<GG, 4>); break;                                \
+    if (split.sw == 5) {                                                                     \
+      if (split.bpw == 1) launch(decode_attention_kernel<GG, 1, 5>);                        \
+      else launch(decode_attention_kernel<GG, 2, 5>);                                        \
+    } else {                                                                                 \
+      switch (split.bpw) {                                                                   \
+        case 1: launch(decode_attention_kernel<GG, 1, 4>); break;                            \
+        case 2: launch(decode_attention_kernel<GG, 2, 4>); break;                            \
+        case 3: launch(decode_attention_kernel<GG, 3, 4>); break;                            \
+        default: launch(decode_attention_kernel<GG, 4, 4>); break;                           \
+      }                                                                                      \
     }                                                                                        \
     break;
   switch (g) {
