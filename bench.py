@@ -107,7 +107,9 @@ def kernel_times(torch, graph, reps: int) -> dict:
     """Average device duration (µs) and launches per replay of each kernel
     in `graph`, from torch.profiler's device activity records over `reps`
     replays: the kernel's own execution time, as rocprofv3's kernel trace
-    reports it (no launch gaps)."""
+    reports it (no launch gaps).  The records can be incomplete when an
+    outside profiler (rocprofv3) holds the same tracing interface; see
+    kernel_us."""
     from collections import defaultdict
     from torch.profiler import ProfilerActivity, profile
     graph.replay()
@@ -121,6 +123,19 @@ def kernel_times(torch, graph, reps: int) -> dict:
         if e.device_type == torch.autograd.DeviceType.CUDA:
             per[e.name].append(e.device_time)
     return {name: {'us': sum(v) / len(v), 'per_replay': len(v) / reps} for name, v in per.items()}
+
+
+def kernel_us(torch, graph, reps: int, launches: int, event_us: float) -> tuple[float, str]:
+    """(µs per launch, source): the kernels' own duration from kernel_times
+    when its records cover the graph's `launches` launches per replay and
+    agree with the event timing `event_us` (per launch, launch gaps
+    included), else `event_us` itself."""
+    kt = kernel_times(torch, graph, reps)
+    seen = sum(v['per_replay'] for v in kt.values())
+    kus = sum(v['us'] * v['per_replay'] for v in kt.values()) / max(launches, 1)
+    if kt and abs(seen - launches) < 0.5 and 0.5 * event_us <= kus <= 1.1 * event_us:
+        return kus, 'kernel'
+    return event_us, 'events'
 
 
 def time_graph(torch, graph, reps: int) -> float:
@@ -484,12 +499,11 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
         with torch.cuda.graph(g):
             fused_pass()
         per = time_graph(torch, g, 10) / len(layers)
-        kt = kernel_times(torch, g, 5)
-        kus = sum(v['us'] * v['per_replay'] for v in kt.values()) / len(layers)
+        kus, src = kernel_us(torch, g, 5, len(layers), per * 1e6)
         b = w4_bytes(1, n, k) + (2 * k if mode == 'SiluMul' else 0) + (2 * n if 'residual' in kw else 0)
         kernels.append({'op': name, 'fusion': mode + (' + residual + sumsq' if 'residual' in kw else ''),
                         'shape': f'{k}->{n}', 'kernel': kernel_name_for((1, n, k), mode), 'bytes': b,
-                        'kernel_us': round(kus, 3), 'us_per_launch': round(per * 1e6, 3),
+                        'kernel_us': round(kus, 3), 'timing': src, 'us_per_launch': round(per * 1e6, 3),
                         'gbs': round(b / kus / 1e3, 1), 'frac': round(b / kus / 1e3 / HBM_PEAK_GBS, 4),
                         'in_decode_step': True, 'launches_per_token': args.layers})
         del g, y
@@ -501,11 +515,10 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
             for w in layers:
                 linear(xs[k], w[name + '._prepared'], y)
         per = time_graph(torch, g, 10) / len(layers)
-        kt = kernel_times(torch, g, 5)
-        kus = sum(v['us'] * v['per_replay'] for v in kt.values()) / len(layers)
+        kus, src = kernel_us(torch, g, 5, len(layers), per * 1e6)
         b = w4_bytes(1, n, k)
         kernels.append({'op': name, 'fusion': 'none (unfused projection)', 'shape': f'{k}->{n}',
-                        'kernel': kernel_name_for((1, n, k)), 'bytes': b, 'kernel_us': round(kus, 3),
+                        'kernel': kernel_name_for((1, n, k)), 'bytes': b, 'kernel_us': round(kus, 3), 'timing': src,
                         'us_per_launch': round(per * 1e6, 3), 'gbs': round(b / kus / 1e3, 1),
                         'frac': round(b / kus / 1e3 / HBM_PEAK_GBS, 4), 'in_decode_step': False,
                         'launches_per_token': args.layers})
@@ -531,13 +544,15 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
     with torch.cuda.graph(g):
         attn_pass()
     per = time_graph(torch, g, 10) / args.layers
-    kt = kernel_times(torch, g, 5)
-    kus = sum(v['us'] * v['per_replay'] for v in kt.values()) / args.layers
+    kt = kernel_times(torch, g, 3)
+    kus, src = kernel_us(torch, g, 5, 2 * args.layers, per * 1e6 / 2)
+    kus *= 2   # the attention launch and its merge launch, per layer
     att_bytes = 2 * kvh * (PROMPT + args.warmup) * 128 * 2 + QKV * 2 + HIDDEN * 2
     kernels.append({'op': 'attention', 'fusion': 'q/k RMSNorm + RoPE + cache append; chunk-merge launch',
                     'shape': f'GQA {cfg.num_attention_heads}/{kvh} x 128, {PROMPT + args.warmup + 1} keys',
                     'kernel': 'decode_attention_kernel + decode_attention_merge_kernel', 'bytes': att_bytes,
-                    'kernel_us': round(kus, 3), 'kernels': {n_[:60]: round(v['us'], 3) for n_, v in kt.items()},
+                    'kernel_us': round(kus, 3), 'timing': src,
+                    'kernels': {n_[:60]: round(v['us'], 3) for n_, v in kt.items()},
                     'us_per_launch': round(per * 1e6, 3), 'gbs': round(att_bytes / kus / 1e3, 1),
                     'frac': round(att_bytes / kus / 1e3 / HBM_PEAK_GBS, 4), 'in_decode_step': True,
                     'launches_per_token': args.layers})
@@ -552,12 +567,12 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
         for _ in range(4):
             native.lm_head(lm_x, model.lm_head, logits=lm_logits, token=lm_tok, workspace=lm_ws)
     per = time_graph(torch, g, 5) / 4
-    kt = kernel_times(torch, g, 5)
-    kus = sum(v['us'] * v['per_replay'] for v in kt.values()) / 4
+    kus, src = kernel_us(torch, g, 5, 8, per * 1e6 / 2)
+    kus *= 2   # the LM head launch and its pick launch
     lm_b = cfg.vocab_size * HIDDEN * 2 + HIDDEN * 2 + cfg.vocab_size * 2
     kernels.append({'op': 'lm_head', 'fusion': 'fp16 GEMV + greedy token (pick launch)',
                     'shape': f'{HIDDEN}->{cfg.vocab_size}', 'kernel': 'lm_head_kernel<10> + lm_head_pick_kernel',
-                    'bytes': lm_b, 'kernel_us': round(kus, 3), 'us_per_launch': round(per * 1e6, 3),
+                    'bytes': lm_b, 'kernel_us': round(kus, 3), 'timing': src, 'us_per_launch': round(per * 1e6, 3),
                     'gbs': round(lm_b / kus / 1e3, 1), 'frac': round(lm_b / kus / 1e3 / HBM_PEAK_GBS, 4),
                     'in_decode_step': True, 'launches_per_token': 1})
     del g
@@ -571,7 +586,8 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
     result['roofline'] = {
         'bound': 'hbm', 'achieved': dom['gbs'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': dom['frac'],
         'traffic': profiled_traffic(dom['kernel'], dom['shape']), 'kernel': dom['kernel'], 'shape': dom['shape'],
-        'op': dom['op'], 'avg_launch_us': dom['kernel_us'], 'graph_us_per_launch': dom['us_per_launch'],
+        'op': dom['op'], 'avg_launch_us': dom['kernel_us'], 'timing': dom['timing'],
+        'graph_us_per_launch': dom['us_per_launch'],
         'algorithmic_bytes_per_launch': dom['bytes'],
         # the metric's second half: the configs[1] GEMV pass, % of HBM peak
         'gemv_pass_pct_hbm_peak': result['gemv_pass']['pct_hbm_peak'],
@@ -590,7 +606,7 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
             linear(xp[k], layers[0][name + '._prepared'], yp)
         sec = time_graph(torch, g, 10)
         graph_sec = sec
-        sec = sum(v['us'] * v['per_replay'] for v in kernel_times(torch, g, 5).values()) / 1e6
+        sec = kernel_us(torch, g, 5, 1, sec * 1e6)[0] / 1e6
         tflops = 2 * 4096 * n * k / sec / 1e12
         # Context, not a target: the vendor library's dense fp16 GEMM
         # (torch.matmul -> hipBLASLt) on the same shape with an fp16
@@ -599,8 +615,8 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
         gv = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gv):
             torch.matmul(xp[k], wt, out=yp)
-        time_graph(torch, gv, 3)
-        vsec = sum(v['us'] * v['per_replay'] for v in kernel_times(torch, gv, 5).values()) / 1e6
+        vsec = time_graph(torch, gv, 10)
+        vsec = kernel_us(torch, gv, 5, 1, vsec * 1e6)[0] / 1e6
         prefill.append({'op': name, 'shape': f'{k}->{n}', 'M': 4096, 'us': round(sec * 1e6, 1),
                         'graph_us': round(graph_sec * 1e6, 1),
                         'tflops': round(tflops, 1), 'frac_fp16_mfma': round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),

@@ -129,15 +129,19 @@ def _status(fn, *args):
 def test_decode_op_argument_checks_on_the_host():
     b = ctypes.c_size_t()
     assert _status('wq_decode_attention_workspace_size', 40, 8, 128, 4224, ctypes.byref(b)) == _native.WQ_OK
-    # 66 sub-chunks of 64 positions -> 33 workgroups of 2 per kv head
-    ml = (8 * 33 * 5 * 2 * 4 + 255) // 256 * 256          # (max, sum) | partial outputs
-    assert b.value == ml + 8 * 33 * 5 * 128 * 4
+    # 264 blocks of 16 positions, 32 chunks wanted per kv head -> 10 blocks per chunk
+    # (five waves x 2), 27 chunks per kv head
+    ml = (8 * 27 * 5 * 2 * 4 + 255) // 256 * 256          # (max, sum) | partial outputs
+    assert b.value == ml + 8 * 27 * 5 * 128 * 4
     assert _status('wq_decode_attention_workspace_size', 32, 4, 128, 9000, ctypes.byref(b)) == _native.WQ_OK
-    ml = (4 * 47 * 8 * 2 * 4 + 255) // 256 * 256          # 141 sub-chunks -> 47 workgroups of 3
-    assert b.value == ml + 4 * 47 * 8 * 128 * 4
+    ml = (4 * 57 * 8 * 2 * 4 + 255) // 256 * 256          # 563 blocks, 64 wanted -> 10 per chunk, 57 chunks
+    assert b.value == ml + 4 * 57 * 8 * 128 * 4
     assert _status('wq_decode_attention_workspace_size', 40, 8, 128, 300, ctypes.byref(b)) == _native.WQ_OK
-    ml = (8 * 5 * 5 * 2 * 4 + 255) // 256 * 256           # 5 sub-chunks -> 5 workgroups of 1
-    assert b.value == ml + 8 * 5 * 5 * 128 * 4
+    ml = (8 * 4 * 5 * 2 * 4 + 255) // 256 * 256           # 19 blocks -> 5 per chunk (one per wave), 4 chunks
+    assert b.value == ml + 8 * 4 * 5 * 128 * 4
+    assert _status('wq_decode_attention_workspace_size', 40, 8, 128, 16384, ctypes.byref(b)) == _native.WQ_OK
+    ml = (8 * 64 * 5 * 2 * 4 + 255) // 256 * 256          # 1024 blocks: four-wave split, 16 per chunk, 64 chunks
+    assert b.value == ml + 8 * 64 * 5 * 128 * 4
     assert _status('wq_decode_attention_workspace_size', 40, 8, 64, 4224, ctypes.byref(b)) == _native.WQ_ERR_UNSUPPORTED
     assert b'head_dim 128' in _native.load().wq_last_error()
     assert _status('wq_decode_attention_workspace_size', 40, 3, 128, 4224, ctypes.byref(b)) == \
