@@ -916,7 +916,15 @@ def main() -> int:
         log('cpu baseline')
         result['cpu_baseline'] = cpu_baseline(torch, native, device, args.layers)
 
-    print(json.dumps(result), flush=True)
+    # Bulky per-case tables first, the decode summary last: a reader that keeps
+    # only the tail of stdout still sees the step's kernels, the GEMV pass, the
+    # roofline and the CPU baseline.
+    last = ('decode_step_kernels', 'int8_e2e', 'e2e_w4_lm_head', 'prefill_seconds', 'prefill_tok_s',
+            'bytes_per_token', 'effective_gbs', 'pct_hbm_peak_effective', 'peak_allocated_gib',
+            'reference_peak_allocated_gib', 'gemv_pass', 'roofline', 'cpu_baseline')
+    ordered = {k: v for k, v in result.items() if k not in last}
+    ordered.update((k, result[k]) for k in last if k in result)
+    print(json.dumps(ordered), flush=True)
     return 0
 
 

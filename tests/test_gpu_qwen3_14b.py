@@ -6,6 +6,9 @@
   QKV GEMM, ``prefill_qk_rope`` and attention over the in-place cache rows,
   then graph-replayed decode steps (fused RMSNorm / SiLU*up / residual GEMVs,
   decode attention, LM head with the greedy token).
+* The full 40-layer model against the oracle: a 64-token prompt and 4 graph
+  decode steps, the oracle's one causal forward over the same 68 tokens
+  (teacher-forced) giving the logits of the same 5 positions.
 * The full 40-layer model with a 4096-token prompt (the benchmark's workload):
   8 graph-replayed decode steps against the eager path (per-layer torch ops,
   the unfused linears and SDPA over the cache) on a second cache holding the
@@ -196,6 +199,85 @@ def test_int8_two_layers_at_14b_geometry_match_oracle(gpu):
     for layer in range(cfg.num_hidden_layers):
         _parity(cache.key_cache[layer][0, :, :516].float().cpu().numpy(), ocache.k[layer],
                 f'int8 K cache layer {layer}')
+
+
+def _oracle_teacher_forced(store, cfg, ids, keep):
+    """The oracle's forward (``oracle/qwen3.py``) over ``ids`` in one causal
+    pass, layer by layer: each layer's seven linears are decoded on host
+    threads a few layers ahead and dropped after use, so the 40-layer model
+    never sits decoded in host memory at once.  fp16 logits of the last
+    ``keep`` positions."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def decoded(idx):
+        np_layer = {k: v.cpu().numpy() for k, v in store.layers[idx].items()}
+        return np_layer, {name: qdq.DecodedLinear(np_layer, name) for name in qwen3.LINEAR_NAMES}
+
+    ids = np.asarray(ids).reshape(-1)
+    hidden = store.embed_tokens.cpu().numpy()[ids].astype(np.float16)
+    cos, sin = qwen3.rotary_tables(cfg.head_dim, cfg.rope_theta, np.arange(ids.size))
+    layers = cfg.num_hidden_layers
+    ahead = 4
+    with ThreadPoolExecutor(max_workers=ahead) as pool:
+        pending = [pool.submit(decoded, i) for i in range(min(ahead, layers))]
+        for idx in range(layers):
+            np_layer, lin = pending[idx].result()
+            pending[idx] = None
+            if idx + ahead < layers:
+                pending.append(pool.submit(decoded, idx + ahead))
+            hidden = qwen3.decoder_layer(hidden, np_layer, cfg, idx, cos, sin, None,
+                                         linear=lambda x, name, _l=lin: _l[name](x))
+            del np_layer, lin
+            if idx % 10 == 9:
+                print(f'[14b-40l-oracle] oracle through layer {idx}', flush=True)
+    hidden = qwen3.rms_norm(hidden[-keep:], store.final_norm.cpu().numpy(), cfg.rms_norm_eps)
+    return qdq.linear_fp32(hidden, store.lm_head.cpu().numpy())
+
+
+def test_forty_layers_match_oracle_teacher_forced(gpu):
+    """configs[4]'s full composition anchored to the oracle: the 40-layer
+    model prefills a 64-token prompt and runs 4 graph-replayed decode steps;
+    the oracle then takes the prompt plus the 4 tokens fed to those steps in
+    one causal forward (prefill of t + 1 tokens == prefill of t + one cached
+    step, the cache invariant), and its logits at the 5 positions the GPU
+    predicted from must agree with the GPU's.  Forty fp16 layers computed in
+    two summation orders (the fused GEMV/GEMM against the oracle's fp16
+    weights with an fp32 dot) drift apart by rounding alone, so the bar is
+    the 40-layer one: cosine >= 0.9995, relative L2 <= 0.03 (measured on
+    MI355X: 0.99996 and 0.009), and the greedy
+    token equal to the oracle's argmax wherever the oracle's top-2 gap
+    exceeds twice the largest logit difference.  A wrong position, head
+    mapping, norm or residual puts the cosine far below the bar."""
+    cfg = _cfg(40)
+    print('[14b-40l-oracle] building the model', flush=True)
+    store, model, _ = _model(cfg, gpu)
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab_size, 64)
+    cache = model.make_resident_cache(batch_size=1, max_seq_len=80)
+    assert cache._decode_graph is not None
+    out = model(torch.from_numpy(prompt)[None].to(gpu), cache=cache, logits_to_keep=1)
+    got = [out.logits[0, -1].float().cpu().numpy()]
+    fed = []
+    token = out.logits[:, -1].argmax(-1, keepdim=True)
+    for step in range(4):
+        fed.append(int(token.item()))
+        out = model(token, cache=cache, logits_to_keep=1)
+        assert out.next_token is not None      # the decode graph ran
+        got.append(out.logits[0, -1].float().cpu().numpy())
+        token = out.next_token
+    assert cache.lengths == [68] * 40
+    print('[14b-40l-oracle] GPU done; oracle forward over 68 tokens', flush=True)
+    ref = _oracle_teacher_forced(store, cfg, np.concatenate([prompt, np.array(fed)]), keep=5).astype(np.float32)
+    decisive = 0
+    for pos, g in enumerate(got):
+        r = ref[pos]
+        m = qdq.parity_metrics(g, r)
+        print(f'[14b-40l-oracle] position {63 + pos}: {m}', flush=True)
+        assert m['finite'] and m['cosine'] >= 0.9995 and m['relative_l2'] <= 0.03, (pos, m)
+        top2 = np.sort(r)[-2:]
+        if top2[1] - top2[0] > 2 * float(np.abs(g - r).max()):
+            assert int(np.argmax(g)) == int(np.argmax(r)), pos
+            decisive += 1
+    print(f'[14b-40l-oracle] decisive positions: {decisive} of 5', flush=True)
 
 
 def test_forty_layers_4096_prompt_graph_against_eager(gpu):
