@@ -115,6 +115,19 @@ int wq_lm_head_workspace_size(int64_t k, int64_t vocab, size_t* bytes);
 int wq_lm_head(const uint16_t* x, int64_t k, const uint16_t* weight, int64_t vocab, uint16_t* logits,
                int64_t* token, void* workspace, size_t workspace_bytes, void* stream);
 
+/* wq_lm_head on the model's final RMSNorm of x, formed inside the LM head
+ * kernel: x is the final residual stream [k] and the LM head reads
+ * norm_weight * fp16(x * rsqrt(sum(sumsq_in) / k + eps)) (fp32 normalize,
+ * fp16 cast, fp16 scale), where sumsq_in holds the sums of squares of x over
+ * 16-element tiles (0 < sumsq_count <= 1024), as the fused decode linears'
+ * residual epilogue writes them.  norm_weight 16-byte aligned.
+ * Replaces: `rms_norm(hidden_states, self.final_norm, eps)` followed by the
+ * LM head and the greedy token (quantized_model.py:331-337, functional.py:17-22,
+ * generation.py:47, :58) for one decode token, without the norm's launch. */
+int wq_lm_head_rmsnorm(const uint16_t* x, int64_t k, const uint16_t* norm_weight, const float* sumsq_in,
+                       int64_t sumsq_count, float eps, const uint16_t* weight, int64_t vocab, uint16_t* logits,
+                       int64_t* token, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes for wq_argmax_f16 (per-wave candidates; no initialization
  * needed). */
 int wq_argmax_f16_workspace_size(int64_t n, size_t* bytes);
@@ -138,12 +151,15 @@ int wq_host_device_pointer(const void* host_ptr, void** device_ptr);
  * [vocab, hidden] (hidden % 8 == 0) for device int64 token ids; table may be
  * the device address of pinned host memory (wq_host_device_pointer), read over
  * the host link.  A token outside [0, vocab) writes NaN and reads nothing.
+ * sumsq_out (may be NULL; hidden % 16 == 0) receives, per row, the fp32 sum of
+ * squares of each 16 consecutive elements ([rows, hidden / 16]): what the
+ * fused decode linears' RMSNorm prologue takes (the first layer's input norm).
  * table and out 16-byte aligned.
  * Replaces: `F.embedding(ids_cpu, self.store.embed_tokens)` + `.to(device)`
  * (quantized_model.py:289-291) for a token id that is already on the device
  * (the previous decode step's greedy token). */
 int wq_embed_rows(const uint16_t* table, int64_t vocab, int64_t hidden, const int64_t* tokens, int64_t rows,
-                  uint16_t* out, void* stream);
+                  uint16_t* out, float* sumsq_out, void* stream);
 
 #ifdef __cplusplus
 }

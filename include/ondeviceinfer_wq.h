@@ -33,7 +33,7 @@ extern "C" {
 #define WQ_ERR_HIP 3              /* HIP runtime error (RuntimeError) */
 #define WQ_ERR_WORKSPACE 4        /* workspace too small (ValueError) */
 
-#define WQ_ABI_VERSION 1
+#define WQ_ABI_VERSION 2
 
 /* Error channel.  The reference raises Python exceptions directly
  * (backend.py:174-175, :212-213, :229-230); the Python host maps codes back. */

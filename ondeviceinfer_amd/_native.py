@@ -28,7 +28,7 @@ WQ_ERR_INVALID_ARGUMENT = 1
 WQ_ERR_UNSUPPORTED = 2
 WQ_ERR_HIP = 3
 WQ_ERR_WORKSPACE = 4
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 W4_BLOCK_K = 128
 DECODE_ATTENTION_MAX_SEQ = 16384   # wq_decode_attention: the largest cache (max_seq) it takes
@@ -85,7 +85,8 @@ _SIGNATURES = {
     'wq_argmax_f16': [_P, _I64, _P, _P, ctypes.c_size_t, _P],
     'wq_lm_head': [_P, _I64, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
     'wq_host_device_pointer': [_P, ctypes.POINTER(ctypes.c_void_p)],
-    'wq_embed_rows': [_P, _I64, _I64, _P, _I64, _P, _P],
+    'wq_embed_rows': [_P, _I64, _I64, _P, _I64, _P, _P, _P],
+    'wq_lm_head_rmsnorm': [_P, _I64, _P, _P, _I64, ctypes.c_float, _P, _I64, _P, _P, _P, ctypes.c_size_t, _P],
 }
 EXPORTED_SYMBOLS = ('wq_last_error', *_SIGNATURES)
 
@@ -808,11 +809,17 @@ def lm_head_workspace_size(k: int, vocab: int) -> int:
 
 def lm_head(x: torch.Tensor, weight: torch.Tensor, *, logits: torch.Tensor | None = None,
             token: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
-            want_logits: bool = True, want_token: bool = True) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+            want_logits: bool = True, want_token: bool = True, norm_weight: torch.Tensor | None = None,
+            sumsq_in: torch.Tensor | None = None, eps: float = 1e-6) -> tuple[torch.Tensor | None, torch.Tensor | None]:
     """fp16 LM head of one token (``x`` [k], ``weight`` [vocab, k]) and its
     greedy token (``torch.argmax`` over the fp16 logits) in one pass:
-    ``wq_lm_head``.  Returns ``(logits [vocab] fp16, token [1] int64)``."""
-    device = _require_gpu(x, weight, logits, token, workspace)
+    ``wq_lm_head``.  Returns ``(logits [vocab] fp16, token [1] int64)``.
+    With ``norm_weight`` and ``sumsq_in`` (fp32 sums of squares of ``x`` over
+    16-element tiles) ``x`` is the final residual stream and the kernel forms
+    the final RMSNorm itself (``wq_lm_head_rmsnorm``)."""
+    device = _require_gpu(x, weight, logits, token, workspace, norm_weight, sumsq_in)
+    if (norm_weight is None) != (sumsq_in is None):
+        raise ValueError('norm_weight and sumsq_in go together')
     if weight.dim() != 2:
         raise ValueError(f'weight must be [vocab, k], got {tuple(weight.shape)}')
     vocab, k = weight.shape
@@ -831,8 +838,16 @@ def lm_head(x: torch.Tensor, weight: torch.Tensor, *, logits: torch.Tensor | Non
         workspace = shared_workspace(device, lm_head_workspace_size(k, vocab), ('lm_head', k, vocab))
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
                                                              workspace.numel() * workspace.element_size())
-    _call('wq_lm_head', _ptr(_aligned(x)), k, _ptr(weight), vocab, _ptr(logits), _ptr(token), ws_ptr, ws_bytes,
-          _stream(device))
+    if norm_weight is None:
+        _call('wq_lm_head', _ptr(_aligned(x)), k, _ptr(weight), vocab, _ptr(logits), _ptr(token), ws_ptr, ws_bytes,
+              _stream(device))
+    else:
+        _check(norm_weight.view(-1), torch.float16, (k,), 'norm_weight')
+        if sumsq_in.dtype != torch.float32 or not sumsq_in.is_contiguous():
+            raise ValueError('sumsq_in must be a contiguous float32 tensor')
+        _call('wq_lm_head_rmsnorm', _ptr(_aligned(x)), k, _ptr(_aligned(norm_weight)), _ptr(sumsq_in),
+              sumsq_in.numel(), float(eps), _ptr(weight), vocab, _ptr(logits), _ptr(token), ws_ptr, ws_bytes,
+              _stream(device))
     return logits, token
 
 
@@ -888,10 +903,13 @@ def host_table(table: torch.Tensor, device: torch.device | str) -> HostTable:
     return HostTable(table, int(ptr.value), device)
 
 
-def embed_rows(table: 'HostTable | torch.Tensor', tokens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def embed_rows(table: 'HostTable | torch.Tensor', tokens: torch.Tensor, out: torch.Tensor | None = None,
+               sumsq_out: torch.Tensor | None = None) -> torch.Tensor:
     """``out[r] = table[tokens[r]]`` (``wq_embed_rows``): the embedding rows of
     device int64 token ids from a ``HostTable`` (read over the host link) or a
-    device fp16 table; an out-of-range id gives a NaN row."""
+    device fp16 table; an out-of-range id gives a NaN row.  ``sumsq_out``
+    (fp32, ``rows * hidden / 16``) receives each row's sums of squares over
+    16-element tiles, the input of the fused linears' RMSNorm prologue."""
     if isinstance(table, HostTable):
         vocab, hidden = table.tensor.shape
         tptr, tdev = table.device_ptr, table.device
@@ -910,5 +928,10 @@ def embed_rows(table: 'HostTable | torch.Tensor', tokens: torch.Tensor, out: tor
         out = torch.empty((rows, hidden), dtype=torch.float16, device=device)
     elif out.dtype != torch.float16 or out.numel() != rows * hidden or not out.is_contiguous():
         raise ValueError(f'out must be a contiguous float16 tensor of {rows * hidden} elements')
-    _call('wq_embed_rows', tptr, vocab, hidden, _ptr(tokens), rows, _ptr(out), _stream(device))
+    if sumsq_out is not None:
+        if (sumsq_out.device != device or sumsq_out.dtype != torch.float32 or not sumsq_out.is_contiguous()
+                or hidden % 16 or sumsq_out.numel() != rows * (hidden // 16)):
+            raise ValueError(f'sumsq_out must be a contiguous float32 tensor of {rows * (hidden // 16)} elements '
+                             'on the tokens\' device (hidden % 16 == 0)')
+    _call('wq_embed_rows', tptr, vocab, hidden, _ptr(tokens), rows, _ptr(out), _ptr(sumsq_out), _stream(device))
     return out

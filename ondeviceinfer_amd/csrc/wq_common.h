@@ -315,6 +315,16 @@ __device__ __forceinline__ float wave_sum_rl(float v) {
   return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
 }
 
+// Eight x values -> w * fp16(x * r), the reference's rms_norm order
+// (normalize in fp32, cast, scale in fp16).
+__device__ __forceinline__ uint4_t rms_scale8(uint4_t xv, uint4_t wv, float r) {
+  const half8_t xh = __builtin_bit_cast(half8_t, xv), wh = __builtin_bit_cast(half8_t, wv);
+  half8_t o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = wh[e] * (half_t)((float)xh[e] * r);
+  return __builtin_bit_cast(uint4_t, o);
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // 2^x on the transcendental unit (v_exp_f32, about 1 ulp; -inf -> 0).

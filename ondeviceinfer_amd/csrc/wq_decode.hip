@@ -525,12 +525,27 @@ int attention_shape_check(int64_t H, int64_t KV, int64_t head_dim, int64_t max_s
 // workgroup per row; a token outside [0, vocab) writes NaN and reads nothing.
 __global__ __launch_bounds__(256) void embed_rows_kernel(const uint4_t* __restrict__ table, int64_t vocab,
                                                          int chunks, const int64_t* __restrict__ tokens,
-                                                         uint4_t* __restrict__ out) {
+                                                         uint4_t* __restrict__ out, float* __restrict__ sumsq) {
   const int64_t t = tokens[blockIdx.x];
   const bool ok = t >= 0 && t < vocab;
   const uint4_t nan8 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
   uint4_t* dst = out + (size_t)blockIdx.x * chunks;
-  for (int c = threadIdx.x; c < chunks; c += 256) dst[c] = ok ? table[(size_t)t * chunks + c] : nan8;
+  // Every lane runs every round (the bound is uniform), so the pairs of
+  // 8-element chunks that make one 16-element sum of squares meet by a lane
+  // swap; lanes past the row only skip their loads and stores.
+  for (int c0 = 0; c0 < chunks; c0 += 256) {
+    const int c = c0 + (int)threadIdx.x;
+    const uint4_t v = c < chunks ? (ok ? table[(size_t)t * chunks + c] : nan8) : uint4_t{0u, 0u, 0u, 0u};
+    if (c < chunks) dst[c] = v;
+    if (sumsq != nullptr) {
+      const half8_t h = __builtin_bit_cast(half8_t, v);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q += (float)h[e] * (float)h[e];
+      q += __shfl_xor(q, 1);
+      if (c < chunks && (c & 1) == 0) sumsq[(size_t)blockIdx.x * (chunks / 2) + c / 2] = q;
+    }
+  }
 }
 
 }  // namespace
@@ -549,16 +564,18 @@ extern "C" int wq_host_device_pointer(const void* host_ptr, void** device_ptr) {
 }
 
 extern "C" int wq_embed_rows(const uint16_t* table, int64_t vocab, int64_t hidden, const int64_t* tokens,
-                             int64_t rows, uint16_t* out, void* stream) {
+                             int64_t rows, uint16_t* out, float* sumsq_out, void* stream) {
   if (rows == 0) return WQ_OK;
   WQ_REQUIRE(table && tokens && out, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
   WQ_REQUIRE(vocab > 0 && hidden > 0 && hidden % 8 == 0 && hidden <= (1 << 24) && rows > 0 && rows <= 65535,
              WQ_ERR_INVALID_ARGUMENT, "need vocab > 0, 0 < hidden, hidden %% 8 == 0, 0 < rows <= 65535");
+  WQ_REQUIRE(sumsq_out == nullptr || (hidden % 16 == 0 && (uintptr_t)sumsq_out % 4 == 0), WQ_ERR_INVALID_ARGUMENT,
+             "sums of squares need hidden %% 16 == 0");
   WQ_REQUIRE(((uintptr_t)table | (uintptr_t)out) % 16 == 0 && (uintptr_t)tokens % 8 == 0, WQ_ERR_INVALID_ARGUMENT,
              "table and out must be 16-byte aligned, tokens 8-byte");
   hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream),
                      reinterpret_cast<const uint4_t*>(table), vocab, (int)(hidden / 8), tokens,
-                     reinterpret_cast<uint4_t*>(out));
+                     reinterpret_cast<uint4_t*>(out), sumsq_out);
   return check_launch("embed_rows");
 }
 

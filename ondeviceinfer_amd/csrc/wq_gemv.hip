@@ -422,16 +422,6 @@ struct FuseArgs {
   float* sumsq_out;        // per-16-row tile sum of squares of y (for the next RmsNorm)
 };
 
-// Eight x values -> w * fp16(x * r), the reference's rms_norm order
-// (normalize in fp32, cast, scale in fp16).
-__device__ __forceinline__ uint4_t rms_scale8(uint4_t xv, uint4_t wv, float r) {
-  const half8_t xh = __builtin_bit_cast(half8_t, xv), wh = __builtin_bit_cast(half8_t, wv);
-  half8_t o;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = wh[e] * (half_t)((float)xh[e] * r);
-  return __builtin_bit_cast(uint4_t, o);
-}
-
 // Eight (gate, up) pairs -> fp16(fp16(silu(gate)) * up), as F.silu on an
 // fp16 tensor followed by an fp16 product (silu in fp32, see silu_f).
 __device__ __forceinline__ uint4_t silu_mul8(uint4_t gv, uint4_t uv) {

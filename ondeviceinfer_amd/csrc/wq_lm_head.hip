@@ -41,16 +41,32 @@ __device__ __forceinline__ bool lm_better(float va, int ia, float vb, int ib) {
 // inside it would leave loads and stores pending together, which forces a
 // full vmcnt wait at every row.  Each wave leaves its best (value, index) in
 // cand[g] for lm_head_pick_kernel.
+// With norm_w, x is the final residual stream and every wave first forms
+// the model's final RMSNorm itself, w * fp16(x * rsqrt(sum(sumsq) / K + eps)),
+// from the per-16-element sums of squares of x that its producer (the last
+// down projection) left in sumsq (count <= 1024): the norm kernel's launch
+// before the LM head is folded in.
 template <int CH>
 __global__ __launch_bounds__(256) void lm_head_kernel(const half_t* __restrict__ x, const half_t* __restrict__ w,
                                                       int V, half_t* __restrict__ logits,
-                                                      float2_t* __restrict__ cand) {
+                                                      float2_t* __restrict__ cand, const half_t* __restrict__ norm_w,
+                                                      const float* __restrict__ sumsq, int sumsq_count, float eps) {
   constexpr int K = CH * kLmChunk;
   const int lane = threadIdx.x & 63;
   const int g = blockIdx.x * 4 + (threadIdx.x >> 6), nw = gridDim.x * 4;
   uint4_t xr[CH];
 #pragma unroll
   for (int j = 0; j < CH; ++j) xr[j] = reinterpret_cast<const uint4_t*>(x)[lane + 64 * j];
+  if (norm_w != nullptr) {
+    uint4_t nr[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) nr[j] = reinterpret_cast<const uint4_t*>(norm_w)[lane + 64 * j];
+    float ss = 0.f;
+    for (int c = lane; c < sumsq_count; c += 64) ss += sumsq[c];
+    const float r = rsqrtf(wave_sum_rl(ss) / (float)K + eps);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) xr[j] = rms_scale8(xr[j], nr[j], r);
+  }
   uint4_t ra[CH], rb[CH];
   auto load = [&](uint4_t (&r)[CH], int row) {
     const uint4_t* p = reinterpret_cast<const uint4_t*>(w + (size_t)min(row, V - 1) * K) + lane;
@@ -203,10 +219,60 @@ int lm_head_check(int64_t k, int64_t vocab) {
   return WQ_OK;
 }
 
+struct LmNorm {
+  const half_t* weight;   // nullptr: x is used as given
+  const float* sumsq;
+  int count;
+  float eps;
+};
+
 template <int CH>
 void launch_lm_head(const half_t* x, const half_t* w, int V, half_t* logits, float2_t* cand, int grid,
-                    hipStream_t s) {
-  hipLaunchKernelGGL(lm_head_kernel<CH>, dim3((unsigned)grid), dim3(256), 0, s, x, w, V, logits, cand);
+                    const LmNorm& nm, hipStream_t s) {
+  hipLaunchKernelGGL(lm_head_kernel<CH>, dim3((unsigned)grid), dim3(256), 0, s, x, w, V, logits, cand, nm.weight,
+                     nm.sumsq, nm.count, nm.eps);
+}
+
+int lm_head_run(const uint16_t* x, int64_t k, const uint16_t* weight, int64_t vocab, uint16_t* logits,
+                int64_t* token, void* workspace, size_t workspace_bytes, const LmNorm& nm, void* stream) {
+  const int rc = lm_head_check(k, vocab);
+  if (rc != WQ_OK) return rc;
+  WQ_REQUIRE(x && weight, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(logits || token, WQ_ERR_INVALID_ARGUMENT, "nothing to compute: logits and token are both NULL");
+  WQ_REQUIRE(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)nm.weight) % 16 == 0 && (uintptr_t)logits % 2 == 0,
+             WQ_ERR_INVALID_ARGUMENT, "x, weight and the norm weight must be 16-byte aligned");
+  const int grid = lm_head_grid(vocab);
+  const size_t need = token ? (size_t)grid * 4 * sizeof(float2_t) : 0;
+  WQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && (uintptr_t)workspace % 8 == 0), WQ_ERR_WORKSPACE,
+             "LM head argmax needs an 8-byte aligned workspace of %zu bytes (got %zu)", need, workspace_bytes);
+  const half_t* xh = reinterpret_cast<const half_t*>(x);
+  const half_t* wh = reinterpret_cast<const half_t*>(weight);
+  half_t* lh = reinterpret_cast<half_t*>(logits);
+  float2_t* cand = token ? reinterpret_cast<float2_t*>(workspace) : nullptr;
+  const hipStream_t s = as_stream(stream);
+  const int V = (int)vocab;
+  switch (k / kLmChunk) {
+    case 1: launch_lm_head<1>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 2: launch_lm_head<2>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 3: launch_lm_head<3>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 4: launch_lm_head<4>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 5: launch_lm_head<5>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 6: launch_lm_head<6>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 7: launch_lm_head<7>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 8: launch_lm_head<8>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 9: launch_lm_head<9>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 10: launch_lm_head<10>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 11: launch_lm_head<11>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 12: launch_lm_head<12>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 13: launch_lm_head<13>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 14: launch_lm_head<14>(xh, wh, V, lh, cand, grid, nm, s); break;
+    case 15: launch_lm_head<15>(xh, wh, V, lh, cand, grid, nm, s); break;
+    default: launch_lm_head<16>(xh, wh, V, lh, cand, grid, nm, s); break;
+  }
+  const int rc1 = check_launch("lm_head");
+  if (rc1 != WQ_OK || !token) return rc1;
+  hipLaunchKernelGGL(lm_head_pick_kernel, dim3(1), dim3(256), 0, s, cand, grid * 4, token);
+  return check_launch("lm_head_pick");
 }
 
 }  // namespace
@@ -224,44 +290,19 @@ extern "C" int wq_lm_head_workspace_size(int64_t k, int64_t vocab, size_t* bytes
 
 extern "C" int wq_lm_head(const uint16_t* x, int64_t k, const uint16_t* weight, int64_t vocab, uint16_t* logits,
                           int64_t* token, void* workspace, size_t workspace_bytes, void* stream) {
-  const int rc = lm_head_check(k, vocab);
-  if (rc != WQ_OK) return rc;
-  WQ_REQUIRE(x && weight, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
-  WQ_REQUIRE(logits || token, WQ_ERR_INVALID_ARGUMENT, "nothing to compute: logits and token are both NULL");
-  WQ_REQUIRE(((uintptr_t)x | (uintptr_t)weight) % 16 == 0 && (uintptr_t)logits % 2 == 0, WQ_ERR_INVALID_ARGUMENT,
-             "x and weight must be 16-byte aligned");
-  const int grid = lm_head_grid(vocab);
-  const size_t need = token ? (size_t)grid * 4 * sizeof(float2_t) : 0;
-  WQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && (uintptr_t)workspace % 8 == 0), WQ_ERR_WORKSPACE,
-             "LM head argmax needs an 8-byte aligned workspace of %zu bytes (got %zu)", need, workspace_bytes);
-  const half_t* xh = reinterpret_cast<const half_t*>(x);
-  const half_t* wh = reinterpret_cast<const half_t*>(weight);
-  half_t* lh = reinterpret_cast<half_t*>(logits);
-  float2_t* cand = token ? reinterpret_cast<float2_t*>(workspace) : nullptr;
-  const hipStream_t s = as_stream(stream);
-  const int V = (int)vocab;
-  switch (k / kLmChunk) {
-    case 1: launch_lm_head<1>(xh, wh, V, lh, cand, grid, s); break;
-    case 2: launch_lm_head<2>(xh, wh, V, lh, cand, grid, s); break;
-    case 3: launch_lm_head<3>(xh, wh, V, lh, cand, grid, s); break;
-    case 4: launch_lm_head<4>(xh, wh, V, lh, cand, grid, s); break;
-    case 5: launch_lm_head<5>(xh, wh, V, lh, cand, grid, s); break;
-    case 6: launch_lm_head<6>(xh, wh, V, lh, cand, grid, s); break;
-    case 7: launch_lm_head<7>(xh, wh, V, lh, cand, grid, s); break;
-    case 8: launch_lm_head<8>(xh, wh, V, lh, cand, grid, s); break;
-    case 9: launch_lm_head<9>(xh, wh, V, lh, cand, grid, s); break;
-    case 10: launch_lm_head<10>(xh, wh, V, lh, cand, grid, s); break;
-    case 11: launch_lm_head<11>(xh, wh, V, lh, cand, grid, s); break;
-    case 12: launch_lm_head<12>(xh, wh, V, lh, cand, grid, s); break;
-    case 13: launch_lm_head<13>(xh, wh, V, lh, cand, grid, s); break;
-    case 14: launch_lm_head<14>(xh, wh, V, lh, cand, grid, s); break;
-    case 15: launch_lm_head<15>(xh, wh, V, lh, cand, grid, s); break;
-    default: launch_lm_head<16>(xh, wh, V, lh, cand, grid, s); break;
-  }
-  const int rc1 = check_launch("lm_head");
-  if (rc1 != WQ_OK || !token) return rc1;
-  hipLaunchKernelGGL(lm_head_pick_kernel, dim3(1), dim3(256), 0, s, cand, grid * 4, token);
-  return check_launch("lm_head_pick");
+  return lm_head_run(x, k, weight, vocab, logits, token, workspace, workspace_bytes, LmNorm{nullptr, nullptr, 0, 0.f},
+                     stream);
+}
+
+extern "C" int wq_lm_head_rmsnorm(const uint16_t* x, int64_t k, const uint16_t* norm_weight, const float* sumsq_in,
+                                  int64_t sumsq_count, float eps, const uint16_t* weight, int64_t vocab,
+                                  uint16_t* logits, int64_t* token, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  WQ_REQUIRE(norm_weight && sumsq_in, WQ_ERR_INVALID_ARGUMENT, "null pointer argument");
+  WQ_REQUIRE(sumsq_count > 0 && sumsq_count <= 1024 && (uintptr_t)sumsq_in % 4 == 0, WQ_ERR_INVALID_ARGUMENT,
+             "need 0 < sumsq_count <= 1024 (got %lld)", (long long)sumsq_count);
+  return lm_head_run(x, k, weight, vocab, logits, token, workspace, workspace_bytes,
+                     LmNorm{reinterpret_cast<const half_t*>(norm_weight), sumsq_in, (int)sumsq_count, eps}, stream);
 }
 
 extern "C" int wq_argmax_f16_workspace_size(int64_t n, size_t* bytes) {

@@ -429,17 +429,16 @@ class DecodeStepGraph:
         eps = cfg.rms_norm_eps
         nat = _native
         lin = self._fused_linear
-        _native.embed_rows(self.embed, self.token, out=self.hidden)
+        # The embedding kernel also leaves the row's per-tile sums of squares,
+        # so the first layer's input RMSNorm rides in its QKV linear like
+        # every later layer's.
+        _native.embed_rows(self.embed, self.token, out=self.hidden, sumsq_out=self.sumsq_down)
         hid = self.hidden.view(-1)
         for idx, w in enumerate(self.layers):
             qkv_p, o_p = w[QKV_FUSED.removesuffix('.weight') + '._prepared'], w['self_attn.o_proj._prepared']
             gu_p, dn_p = w[GATE_UP_FUSED.removesuffix('.weight') + '._prepared'], w['mlp.down_proj._prepared']
-            if idx == 0:
-                nat.add_rmsnorm(self.hidden, w['input_layernorm.weight'], eps, out=self.states)
-                lin(self.states.view(-1), qkv_p, out=self.qkv)
-            else:
-                lin(hid, qkv_p, x_mode=nat.X_RMSNORM, norm_weight=w['input_layernorm.weight'],
-                    sumsq_in=self.sumsq_down, eps=eps, out=self.qkv)
+            lin(hid, qkv_p, x_mode=nat.X_RMSNORM, norm_weight=w['input_layernorm.weight'],
+                sumsq_in=self.sumsq_down, eps=eps, out=self.qkv)
             nat.decode_attention(self.qkv.view(-1), cfg.num_attention_heads, cfg.num_key_value_heads,
                                  w['self_attn.q_norm.weight'], w['self_attn.k_norm.weight'], eps, self.cos,
                                  self.sin, self.position, self.kc[idx], self.vc[idx], self.scale, out=self.attn,
@@ -449,6 +448,13 @@ class DecodeStepGraph:
                 sumsq_in=self.sumsq_o, eps=eps, out=self.gate_up)
             lin(self.gate_up.view(-1), dn_p, x_mode=nat.X_SILU_MUL, residual=hid, sumsq_out=self.sumsq_down,
                 out=hid)
+        if self.lm_w4 is None and self.native_lm_head:
+            # The final RMSNorm inside the LM head, from the last down
+            # projection's sums of squares.
+            _native.lm_head(hid, self.model.lm_head, logits=self.logits.view(-1), token=self.next_token,
+                            workspace=self.lm_ws, norm_weight=self.model.final_norm, sumsq_in=self.sumsq_down,
+                            eps=eps)
+            return
         nat.add_rmsnorm(self.hidden, self.model.final_norm, eps, out=self.states)
         self._lm_head()
 

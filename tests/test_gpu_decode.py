@@ -273,6 +273,19 @@ def test_embed_rows(nat, on_host):
     torch.cuda.synchronize()
     bad = bad.cpu()
     assert torch.equal(bad[0], table[3]) and bool(torch.isnan(bad[1:]).all())
+    # The per-16-element sums of squares the first layer's fused RMSNorm takes.
+    sq = torch.full((ids.numel() * hidden // 16,), -1.0, device='cuda')
+    again = nat.embed_rows(src, ids, sumsq_out=sq)
+    torch.cuda.synchronize()
+    assert torch.equal(again.cpu(), table[ids.cpu()])
+    ref = (table[ids.cpu()].double() ** 2).view(ids.numel(), hidden // 16, 16).sum(-1).view(-1)
+    assert torch.allclose(sq.cpu().double(), ref, rtol=1e-6, atol=0)
+    sq_bad = torch.zeros(3 * hidden // 16, device='cuda')
+    nat.embed_rows(src, torch.tensor([3, -1, 1000], dtype=torch.long, device='cuda'), sumsq_out=sq_bad)
+    sq_bad = sq_bad.cpu().view(3, -1)
+    assert bool(torch.isfinite(sq_bad[0]).all()) and bool(torch.isnan(sq_bad[1:]).all())
+    with pytest.raises(ValueError):
+        nat.embed_rows(src, ids, sumsq_out=torch.zeros(7, device='cuda'))
     with pytest.raises(ValueError):
         nat.host_table(table.cuda(), 'cuda:0')
 
@@ -423,6 +436,32 @@ def test_lm_head_logits_and_token(nat, vocab, k):
         top2 = np.sort(ref.astype(np.float32))[-2:]
         if top2[1] - top2[0] > 4e-3 * max(abs(top2[1]), 1.0):
             assert token.item() == int(np.argmax(ref))
+
+
+@pytest.mark.parametrize('vocab,k', [(1000, 512), (151936, 5120)])
+def test_lm_head_with_final_rmsnorm(nat, vocab, k):
+    """wq_lm_head_rmsnorm: the final RMSNorm formed inside the LM head from
+    the residual stream and its per-16-element sums of squares, against the
+    oracle's rms_norm followed by the fp32-accumulated LM head; the token is
+    argmax of the returned logits."""
+    from oracle import qwen3
+    print(f'[lm_head_rmsnorm] vocab={vocab} k={k}', flush=True)
+    rng = np.random.default_rng(vocab + k + 1)
+    x = (rng.standard_normal(k) * 3.0).astype(np.float16)
+    nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float16)
+    w = (rng.standard_normal((vocab, k)) * 0.05).astype(np.float16)
+    sq = (x.astype(np.float32) ** 2).reshape(-1, 16).sum(-1).astype(np.float32)
+    eps = 1e-6
+    tw = torch.from_numpy(w).cuda()
+    logits, token = nat.lm_head(torch.from_numpy(x).cuda(), tw, norm_weight=torch.from_numpy(nw).cuda(),
+                                sumsq_in=torch.from_numpy(sq).cuda(), eps=eps)
+    torch.cuda.synchronize()
+    ref = qdq.linear_fp32(qwen3.rms_norm(x[None], nw, eps), w)[0]
+    m = qdq.parity_metrics(logits.cpu().numpy(), ref)
+    assert qdq.parity_ok(m), m
+    assert token.item() == int(torch.argmax(logits).item())
+    with pytest.raises(ValueError):
+        nat.lm_head(torch.from_numpy(x).cuda(), tw, norm_weight=torch.from_numpy(nw).cuda())
 
 
 def test_lm_head_ties_nan_and_infinities(nat):
