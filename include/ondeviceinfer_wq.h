@@ -96,14 +96,18 @@ int wq_w4_decode_rows(const int32_t* weight_packed, const float* weight_scale,
                       uint16_t* weight, void* stream);
 
 /* Workspace bytes wq_w4a16_linear can use for this shape (0 when it needs
- * none).  The workspace holds the per-tile counters and fp32 partials of the
- * decode GEMV when a tile's k range is split over several workgroups.  It must
- * be zero-filled once before first use; every call leaves it zeroed again, so
- * it can be reused by later calls (and graph replays) on the same stream.
- * Calls that may run concurrently need separate workspaces.  With a NULL or
- * smaller workspace the kernels keep each tile in one workgroup (same result,
- * slower for short-N shapes).  Replaces marlin_make_workspace_new
- * (backend.py:223). */
+ * none).  The workspace holds the arrival counters and fp32 partials of the
+ * kernels that split a tile's k range over several workgroups: the decode
+ * GEMV (m <= 4) and the small-batch kernel (12 <= m <= 32 on n <= 12288).
+ * The counters sit in a fixed region at the start, so one buffer sized for
+ * the largest shape serves every shape.  It must be zero-filled once before
+ * first use; every call leaves the counters zeroed again, so it can be
+ * reused by later calls (and graph replays) on the same stream.  Calls that
+ * may run concurrently need separate workspaces.  With a NULL or smaller
+ * workspace the linear runs without the split (the decode GEMV keeps each
+ * tile in one workgroup: same result; at 12 <= m <= 32 the skinny kernels:
+ * the same values up to fp32 summation order).  Replaces
+ * marlin_make_workspace_new (backend.py:223). */
 int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t group_size, size_t* bytes);
 
 /* y fp16 [m, n] = x fp16 [m, k] . dequant(W)^T with fp32 accumulation.
@@ -114,7 +118,7 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* wq_w4a16_linear without a workspace argument and without any allocation:
- * the decode GEMV's k-split counters and partials live in a fixed 4 MiB
+ * the k-split counters and partials live in a fixed 4 MiB
  * device array inside the library (one per GPU, held until the process
  * ends), so the call is as fast as wq_w4a16_linear with its workspace.
  * Every call on a GPU shares that GPU's array: calls that may overlap on one
@@ -123,9 +127,12 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
  * (hipGetSymbolAddress) and queues a clear of it on `stream`; that first call
  * must not be under stream capture (it returns WQ_ERR_UNSUPPORTED there, so
  * no clear is ever recorded into a graph): make one eager call per device
- * before capturing later ones, which then record only the linear.  Shapes whose
- * split plan would need more than 4 MiB return WQ_ERR_WORKSPACE (none of the
- * planner's current shapes do: its largest split needs 2 MiB).
+ * before capturing later ones, which then record only the linear.  Decode
+ * shapes (m <= 4) whose split plan would need more than 4 MiB return
+ * WQ_ERR_WORKSPACE (none of the planner's current shapes do: its largest
+ * split needs 2 MiB); a small-batch plan (12 <= m <= 32) that does not fit
+ * runs the skinny kernels instead, as wq_w4a16_linear does with a short
+ * workspace.
  * No counterpart in the reference: it exists for callers that cannot
  * allocate (code under HIP graph capture, serving loops and harnesses that
  * forbid hipMalloc). */

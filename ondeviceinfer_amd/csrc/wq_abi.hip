@@ -18,6 +18,7 @@ void set_error(const char* fmt, ...) {
 }
 
 size_t gemv_workspace_bytes(bool w4, int64_t m, int64_t n, int64_t k);
+size_t w4_batch_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t g);
 int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                      half_t* y, void* ws, size_t ws_bytes, hipStream_t s);
 int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
@@ -82,8 +83,8 @@ extern "C" int wq_abi_version(void) { return WQ_ABI_VERSION; }
 extern "C" int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t group_size, size_t* bytes) {
   if (int st = linear_shape_check(m, n, k)) return st;
   WQ_REQUIRE(bytes, WQ_ERR_INVALID_ARGUMENT, "null size output");
-  (void)group_size;
-  *bytes = gemv_workspace_bytes(true, m, n, k);
+  const size_t flat = gemv_workspace_bytes(true, m, n, k), batch = w4_batch_workspace_bytes(m, n, k, group_size);
+  *bytes = flat > batch ? flat : batch;
   return WQ_OK;
 }
 
@@ -392,7 +393,11 @@ extern "C" int wq_w4a16_linear_noalloc(const uint16_t* x, int64_t m, int64_t k, 
                                        int64_t n, int64_t group_size, uint16_t* y, void* stream) {
   if (int st = linear_shape_check(m, n, k)) return st;
   if (m == 0) return wq_w4a16_linear(x, m, k, tiles, meta, n, group_size, y, nullptr, 0, stream);
-  const size_t need = gemv_workspace_bytes(true, m, n, k);
+  size_t need = gemv_workspace_bytes(true, m, n, k);
+  // The small-batch kernel's partials (5 <= m <= 32) when they fit; beyond
+  // that the linear runs the skinny kernels, which need no scratch.
+  const size_t batch = w4_batch_workspace_bytes(m, n, k, group_size);
+  if (batch > need && batch <= kNoAllocScratchBytes) need = batch;
   WQ_REQUIRE(need <= kNoAllocScratchBytes, WQ_ERR_WORKSPACE,
              "wq_w4a16_linear_noalloc: m=%lld n=%lld k=%lld needs %zu scratch bytes, more than the %zu it holds",
              (long long)m, (long long)n, (long long)k, need, kNoAllocScratchBytes);

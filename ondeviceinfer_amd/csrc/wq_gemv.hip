@@ -921,6 +921,9 @@ int launch_w4_gemv_flat(const half_t* x, int M, int K, const uint4_t* tiles, con
 
 }  // namespace
 
+int launch_w4_batch(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
+                    void* ws, size_t ws_bytes, hipStream_t st);
+
 int launch_w4_gemv_fused(const half_t* x, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G,
                          int x_mode, const half_t* norm_w, const float* sumsq_in, int sumsq_count, float eps,
                          const half_t* residual, float* sumsq_out, half_t* y, void* ws, size_t ws_bytes,
@@ -959,6 +962,10 @@ int launch_w4_skinny(const half_t* x, int M, int K, const uint4_t* tiles, const 
                      half_t* y, void* ws, size_t ws_bytes, hipStream_t s) {
   if (M <= kGemvFlatMaxM) {
     int rc = launch_w4_gemv_flat(x, M, K, tiles, meta, N, G, y, ws, ws_bytes, s);
+    if (rc != kNotApplicable) return rc;
+  } else {
+    // 12 <= M <= 32 on narrow N: activations shared in LDS (wq_batch.hip).
+    int rc = launch_w4_batch(x, M, K, tiles, meta, N, G, y, ws, ws_bytes, s);
     if (rc != kNotApplicable) return rc;
   }
   const int mc = (M + 15) / 16;

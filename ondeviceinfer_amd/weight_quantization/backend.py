@@ -138,8 +138,11 @@ class NativeOps:
 
     @staticmethod
     def w4a16_linear(x: torch.Tensor, prepared: PreparedW4, output: torch.Tensor | None = None) -> torch.Tensor:
+        # The prepared workspace is sized for the decode GEMV (M <= 4); larger
+        # batches take the library's shared workspace for their own plans.
+        ws = prepared.workspace if x.shape[0] <= 4 else None
         return _native.w4a16_linear(x, prepared.tiles, prepared.meta, prepared.n, prepared.group_size,
-                                    out=output, workspace=prepared.workspace)
+                                    out=output, workspace=ws)
 
     @staticmethod
     def w8a16_linear(x: torch.Tensor, prepared: PreparedW8, output: torch.Tensor | None = None) -> torch.Tensor:
