@@ -123,13 +123,6 @@ __global__ __launch_bounds__(1024) void w8a8_gemv_kernel(const int8_t* __restric
   }
 }
 
-// 16 bytes per lane global -> LDS (global_load_lds_dwordx4): lane L's bytes
-// land at lds_base + 16 * L.  Kept out of the kernel template: with the
-// builtin written inside it, the host pass drops the kernel's launch stub.
-__device__ __forceinline__ void i8_lds_load16(const void* src, uint8_t* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
-}
-
 // LDS slot of 16-byte chunk c (0..7) in row r of a 128-byte stage row: rows
 // 2 apart share banks, so the slot is permuted by r / 2; the sixteen rows a
 // B-fragment read touches then hit sixteen distinct 16-byte bank groups.
@@ -137,6 +130,26 @@ __device__ __forceinline__ int i8_swz(int r, int c) { return c ^ ((r >> 1) & 7);
 
 constexpr int kI8Blk = 128;              // k per GEMM stage (two int8 MFMA steps)
 constexpr int kI8RowBytes = kI8Blk;      // one int8 x row per stage
+
+// The MT B-fragments of one 64-k step, fragment mt from row mt*16 + i of the
+// stage: a per-lane address plus the immediate mt * 16 rows.  Inline asm,
+// as in the W4 GEMM: a read the compiler can see makes it wait for every
+// outstanding buffer -> LDS copy (vmcnt(0)) first, the next stage's included,
+// which serializes the copies with the math; these reads are completed by
+// lds_wait_first_half / lds_wait_rest.
+template <int OFF>
+__device__ __forceinline__ uint4_t i8_lds_read_off(uint32_t a) {
+  uint4_t v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+template <int MT, int MTI = 0>
+__device__ __forceinline__ void i8_read_frags(uint4_t (&b)[MT], uint32_t a) {
+  if constexpr (MTI < MT) {
+    b[MTI] = i8_lds_read_off<MTI * 16 * kI8RowBytes>(a);
+    i8_read_frags<MT, MTI + 1>(b, a);
+  }
+}
 
 // M > 16: grid = (ceil(tiles / (4 NT)), ceil(M / BM)), 256 threads, BM = 16 MT.
 // Wave w owns the NT 16-row weight tiles (4 bx + w) NT .. +NT-1 (disjoint
@@ -168,10 +181,17 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
   const int nblk = K / kI8Blk;
   const int m0 = blockIdx.y * BM;
   const int tile0 = ((int)blockIdx.x * 4 + wave) * NT;
-  const int8_t* wrow[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) wrow[t] = qw + wl8.lane_base(min(tile0 + t, ntile - 1), lane, N, K);
-  const int blk_bytes = wl8.block_bytes(), p1 = wl8.piece1();
+  // Every load goes through a buffer resource with a wave-uniform base and
+  // 32-bit offsets (K <= 2^23, checked by the host): rows past M and tiles
+  // past N fall outside the buffers and read as zero (never stored).  With
+  // plain global loads of the weights the compiler put a vmcnt(0) before
+  // each block's first MFMA, waiting for the next block's loads as well.
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(qx + (size_t)m0 * K, (int64_t)(M - m0) * K);
+  const __amdgpu_buffer_rsrc_t rw =
+      wl8.tiled ? buf_rsrc(qw + (size_t)tile0 * nblk * kW8TileBlockBytes, (int64_t)(ntile - tile0) * nblk * kW8TileBlockBytes)
+                : buf_rsrc(qw + (size_t)tile0 * 16 * K, (int64_t)(N - tile0 * 16) * K);
+  const uint32_t w_voff = wl8.tiled ? (uint32_t)lane * 16 : (uint32_t)(i * K + 16 * kb);
+  const uint32_t w_p1 = (uint32_t)wl8.piece1();
 
   // Stage `st` <- x rows m0 .. m0+BM-1, k block `blk`: instruction J of the
   // workgroup fills bytes [1024 J, 1024 J + 1024), i.e. rows 8J .. 8J+7;
@@ -183,16 +203,16 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
       const int J = wave * kInstrPerWave + j;
       const int r = 8 * J + (lane >> 3);
       const int c = i8_swz(r, lane & 7);
-      const int8_t* src = qx + (size_t)min(m0 + r, M - 1) * K + (size_t)blk * kI8Blk + 16 * c;
-      i8_lds_load16(src, xs + st * kStageBytes + J * 1024);
+      lds_load16(rx, (uint32_t)(r * K + 16 * c), (uint32_t)(blk * kI8Blk), xs + st * kStageBytes + J * 1024);
     }
   };
   auto fetch_w = [&](int blk, uint4_t (&r)[NT][2]) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int8_t* p = wrow[t] + (size_t)blk * blk_bytes;
-      r[t][0] = *reinterpret_cast<const uint4_t*>(p);        // k + 16 kb .. +15
-      r[t][1] = *reinterpret_cast<const uint4_t*>(p + p1);   // k + 64 + 16 kb .. +15
+      const uint32_t so = wl8.tiled ? (uint32_t)((t * nblk + blk) * kW8TileBlockBytes)
+                                    : (uint32_t)(t * 16 * K + blk * kI8Blk);
+      r[t][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff, so, 0);          // k + 16 kb .. +15
+      r[t][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff + w_p1, so, 0);   // k + 64 + 16 kb .. +15
     }
   };
 
@@ -203,6 +223,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = int4v_t{0, 0, 0, 0};
 
   uint4_t cur[NT][2], nxt[NT][2];
+  const uint32_t xs_lds = (uint32_t)(size_t)((const __attribute__((address_space(3))) uint8_t*)xs);
   copy_x(0, 0);
   fetch_w(0, cur);
   __builtin_amdgcn_s_waitcnt(0);   // stage 0 landed
@@ -214,17 +235,24 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
       copy_x(blk + 1, st ^ 1);
       fetch_w(blk + 1, nxt);
     }
-    const uint8_t* stage = xs + st * kStageBytes;
+    // Row r = mt*16 + i of the stage holds chunk c at slot i8_swz(r, c) =
+    // c ^ ((i >> 1) & 7): one lane address per step, mt in the offset.
+    const uint32_t stage = xs_lds + (uint32_t)(st * kStageBytes + i * kI8RowBytes);
 #pragma unroll
     for (int step = 0; step < 2; ++step) {
       const int c = 4 * step + kb;   // 16-byte chunk of this lane's k range
+      uint4_t b[MT];
+      i8_read_frags<MT>(b, stage + (uint32_t)(i8_swz(i, c) * 16));
+      lds_wait_first_half<MT>(b);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int r = mt * 16 + i;
-        const uint4_t b = *reinterpret_cast<const uint4_t*>(stage + r * kI8RowBytes + i8_swz(r, c) * 16);
+      for (int mt = 0; mt < (MT + 1) / 2; ++mt)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b, acc[t][mt]);
-      }
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b[mt], acc[t][mt]);
+      lds_wait_rest<MT>(b);
+#pragma unroll
+      for (int mt = (MT + 1) / 2; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b[mt], acc[t][mt]);
     }
     if (more) {
 #pragma unroll
@@ -254,6 +282,10 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
 }
 
 constexpr int kW8A8GemvMaxM = 16;
+// Largest k of the W8A8 GEMM: its x and weight offsets are 32-bit (127 rows
+// of k bytes, 64 weight rows of k bytes); longer rows run the GEMV kernel 16
+// rows at a time.
+constexpr int64_t kW8A8GemmMaxK = 1 << 23;
 
 }  // namespace
 }  // namespace wq
@@ -287,7 +319,7 @@ int w8a8_linear_impl(const int8_t* qx, const float* x_scale, int64_t m, int64_t 
   const half_t* b = reinterpret_cast<const half_t*>(bias);
   half_t* yy = reinterpret_cast<half_t*>(y);
   const int64_t nsteps = k / kI8Step, ntile = (n + 15) / 16;
-  if (m > kW8A8GemvMaxM && k % kI8Blk == 0) {
+  if (m > kW8A8GemvMaxM && k % kI8Blk == 0 && k <= kW8A8GemmMaxK) {
     // GEMM: 128-row x tiles for long batches, 32-row ones otherwise; four
     // weight tiles per wave while that still leaves a full machine of
     // workgroups, else one.  Over INT8 tiles, long batches take two tiles
@@ -315,7 +347,7 @@ int w8a8_linear_impl(const int8_t* qx, const float* x_scale, int64_t m, int64_t 
   // Decode kernel: about eight 64-k steps per wave (one round of loads).
   int ksw = (int)((nsteps + 7) / 8);
   ksw = ksw < 1 ? 1 : (ksw > 16 ? 16 : ksw);
-  for (int64_t r = 0; r < m; r += kW8A8GemvMaxM) {   // batches beyond 16 rows only when k % 128 != 0
+  for (int64_t r = 0; r < m; r += kW8A8GemvMaxM) {   // batches beyond 16 rows only when k % 128 != 0 or k > 2^23
     const int64_t mr = m - r < kW8A8GemvMaxM ? m - r : kW8A8GemvMaxM;
     hipLaunchKernelGGL(w8a8_gemv_kernel, dim3((unsigned)ntile), dim3(64 * ksw), 0, as_stream(stream), qx + r * k,
                        x_scale + r, (int)mr, (int)k, qweight, w_scale, b, (int)n, yy + r * n, wl8);
