@@ -98,7 +98,7 @@ int wq_w4_decode_rows(const int32_t* weight_packed, const float* weight_scale,
 /* Workspace bytes wq_w4a16_linear can use for this shape (0 when it needs
  * none).  The workspace holds the arrival counters and fp32 partials of the
  * kernels that split a tile's k range over several workgroups: the decode
- * GEMV (m <= 4) and the small-batch kernel (12 <= m <= 32 on n <= 12288).
+ * GEMV (m <= 4) and the small-batch kernel (12 <= m <= 32 on n <= 18432).
  * The counters sit in a fixed region at the start, so one buffer sized for
  * the largest shape serves every shape.  It must be zero-filled once before
  * first use; every call leaves the counters zeroed again, so it can be

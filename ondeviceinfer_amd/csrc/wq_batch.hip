@@ -1,4 +1,4 @@
-// Small-batch W4A16 linear (12 <= M <= 32) for narrow N (at most 768 tiles):
+// Small-batch W4A16 linear (12 <= M <= 32) for N up to 1152 tiles (18432 rows):
 // the activation slice is staged once per workgroup in LDS and shared by its
 // eight waves, which own eight different 16-row tiles.
 //
@@ -29,10 +29,12 @@ namespace wq {
 namespace {
 
 constexpr int kBatchWaves = 8;                         // waves (tiles) per workgroup
-constexpr int kBatchMaxTiles = 768;                    // narrow N only; wider shapes keep the ring kernels
+// Up to the gate / up projections (1088 tiles).  The fused gate_up (2176
+// tiles) keeps the skinny ring (M <= 16) and the deep-ring GEMM (M > 16):
+// there this kernel's 1088 workgroups at M = 32 took 46 us against 37.
+constexpr int kBatchMaxTiles = 1152;
 constexpr int kBatchMaxGroups = kBatchMaxTiles / kBatchWaves;
 constexpr size_t kBatchCounterBytes = 256 * ((4 * kBatchMaxGroups + 255) / 256);
-constexpr int kComputeUnits = 256;
 // Below 12 rows the skinny kernels stay ahead: the k split's publish, count
 // and sum steps cost about 3 us per launch, more than the shared x saves
 // there (MI355X, fused QKV 5120->7168: M = 8 9.9 against 9.1 us; M = 16
@@ -241,9 +243,11 @@ struct BatchPlan {
 };
 
 // The plan for (M, N, K) or r == 0 when this kernel does not take the shape:
-// the longest k range R (fewest partials) whose grid is resident in one
-// round, one eight-wave workgroup per compute unit (the R = 8 and 10 forms
-// take more than 128 registers, and their x slices up to 80 KiB of LDS).
+// the longest k range R (fewest partials) with at most 16 splits.  The
+// narrow shapes then run one eight-wave workgroup per compute unit (fused
+// QKV 224 workgroups, q/o 160); the gate and up projections (1088 tiles)
+// run 544 workgroups in about two rounds, still ahead of the skinny ring
+// (MI355X, 5120->17408: M = 16 25.2 -> 17.9-20.0 us, M = 32 31.8 -> 27.1 us).
 BatchPlan batch_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
   BatchPlan p{(int)((M + 15) / 16), 0, 0, 0};
   const int64_t ntile = (N + 15) / 16, nblk = K / kW4BlockK;
@@ -254,7 +258,7 @@ BatchPlan batch_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
   for (int r : {10, 8, 5, 4}) {
     if (nblk % r != 0) continue;
     const int s = (int)(nblk / r);
-    if (s > 16 || (int64_t)p.groups * s > kComputeUnits) continue;
+    if (s > 16) continue;
     if ((r * p.mc * 4) % kBatchWaves != 0) continue;
     p.r = r;
     p.s = s;

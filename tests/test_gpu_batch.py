@@ -46,9 +46,10 @@ def prepared(n, k, m, seed, gpu, group_size=128, symmetric=False):
 
 # (n, k, group, symmetric): the fused QKV and q/o shapes (4 splits of 10 blocks), k/v
 # (8 tiles: one workgroup per split), a partial last tile group (1000 rows = 63 tiles,
-# one split of 8 blocks), and group 256 with two splits of 10 blocks.
+# one split of 8 blocks), group 256 with two splits of 10 blocks, and the gate / up
+# projection (136 tile groups x 4 splits, about two rounds of workgroups).
 SHAPES = [(7168, 5120, 128, False), (5120, 5120, 128, False), (1024, 5120, 128, True), (1000, 1024, 128, False),
-          (2048, 2560, 256, False)]
+          (2048, 2560, 256, False), (17408, 5120, 128, False)]
 
 
 @pytest.mark.parametrize('n,k,g,sym', SHAPES)
@@ -68,7 +69,8 @@ def test_batch_plans_use_the_workspace_and_fall_back_without_it(gpu):
     back at zero after the calls."""
     n, k, m = 7168, 5120, 32
     assert _native.w4a16_workspace_size(m, n, k, 128) > 0
-    assert _native.w4a16_workspace_size(m, 17408, k, 128) == 0   # wide N keeps the ring kernels
+    assert _native.w4a16_workspace_size(m, 17408, k, 128) > 0    # gate / up (1088 tiles)
+    assert _native.w4a16_workspace_size(m, 34816, k, 128) == 0   # the fused gate_up keeps the ring kernels
     assert _native.w4a16_workspace_size(33, n, k, 128) == 0      # beyond M = 32
     assert _native.w4a16_workspace_size(11, n, k, 128) == 0      # below M = 12 (skinny kernels)
     assert _native.w4a16_workspace_size(12, n, k, 128) > 0
