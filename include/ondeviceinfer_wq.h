@@ -98,15 +98,17 @@ int wq_w4_decode_rows(const int32_t* weight_packed, const float* weight_scale,
 /* Workspace bytes wq_w4a16_linear can use for this shape (0 when it needs
  * none).  The workspace holds the arrival counters and fp32 partials of the
  * kernels that split a tile's k range over several workgroups: the decode
- * GEMV (m <= 4) and the small-batch kernel (12 <= m <= 32 on n <= 18432).
- * The counters sit in a fixed region at the start, so one buffer sized for
+ * GEMV (m <= 4), the small-batch kernel (12 <= m <= 32 on n <= 18432) and the
+ * deep-ring GEMM on the smallest prefill grids (m > 64 on narrow n).  The
+ * counters sit in a fixed 16 KiB region at the start, so one buffer sized for
  * the largest shape serves every shape.  It must be zero-filled once before
  * first use; every call leaves the counters zeroed again, so it can be
  * reused by later calls (and graph replays) on the same stream.  Calls that
  * may run concurrently need separate workspaces.  With a NULL or smaller
  * workspace the linear runs without the split (the decode GEMV keeps each
- * tile in one workgroup: same result; at 12 <= m <= 32 the skinny kernels:
- * the same values up to fp32 summation order).  Replaces
+ * tile in one workgroup: same result; at 12 <= m <= 32 the skinny kernels,
+ * and the deep-ring GEMM over the whole k range: the same values up to fp32
+ * summation order).  Replaces
  * marlin_make_workspace_new (backend.py:223). */
 int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t group_size, size_t* bytes);
 
@@ -130,9 +132,9 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
  * before capturing later ones, which then record only the linear.  Decode
  * shapes (m <= 4) whose split plan would need more than 4 MiB return
  * WQ_ERR_WORKSPACE (none of the planner's current shapes do: its largest
- * split needs 2 MiB); a small-batch plan (12 <= m <= 32) that does not fit
- * runs the skinny kernels instead, as wq_w4a16_linear does with a short
- * workspace.
+ * split needs 2 MiB); a small-batch plan (12 <= m <= 32) or a deep-ring GEMM
+ * split (the smallest prefill grids) that does not fit runs without the split
+ * instead, as wq_w4a16_linear does with a short workspace.
  * No counterpart in the reference: it exists for callers that cannot
  * allocate (code under HIP graph capture, serving loops and harnesses that
  * forbid hipMalloc). */

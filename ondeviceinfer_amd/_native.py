@@ -326,11 +326,13 @@ def w4a16_linear(x: torch.Tensor, tiles: torch.Tensor, meta: torch.Tensor, n: in
             raise ValueError('out must be 16-byte aligned')
     if workspace is None and m <= 4:
         workspace = shared_workspace(device, w4a16_workspace_size(m, n, k, group_size), ('w4a16', m, n, k, group_size))
-    elif workspace is None and m <= 32:
-        # The small-batch kernel's partials; its counters sit in a fixed
-        # region at the front and are zero after every call, so all its
-        # shapes share one buffer.
-        workspace = shared_workspace(device, w4a16_workspace_size(m, n, k, group_size), ('w4a16-batch',))
+    elif workspace is None:
+        # The small-batch kernel's and the deep-ring GEMM's split partials:
+        # their counters sit in a fixed region at the front and are zero
+        # after every call, so all such shapes share one buffer.
+        nbytes = w4a16_workspace_size(m, n, k, group_size)
+        if nbytes:
+            workspace = shared_workspace(device, nbytes, ('w4a16-split',))
     ws_ptr, ws_bytes = None, 0
     if workspace is not None:
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()

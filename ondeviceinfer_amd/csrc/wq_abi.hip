@@ -26,7 +26,8 @@ int launch_w8_skinny(const half_t* x, int M, int K, const int8_t* q, const half_
 int launch_w8_generic(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
                       half_t* y, hipStream_t s);
 int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
-                   hipStream_t s);
+                   hipStream_t s, void* ws, size_t ws_bytes);
+size_t w4_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
 int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
                    half_t* y, hipStream_t s, int tiled);
 bool w4_gemm_small_fits(int64_t M, int64_t N);
@@ -83,8 +84,12 @@ extern "C" int wq_abi_version(void) { return WQ_ABI_VERSION; }
 extern "C" int wq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int64_t group_size, size_t* bytes) {
   if (int st = linear_shape_check(m, n, k)) return st;
   WQ_REQUIRE(bytes, WQ_ERR_INVALID_ARGUMENT, "null size output");
-  const size_t flat = gemv_workspace_bytes(true, m, n, k), batch = w4_batch_workspace_bytes(m, n, k, group_size);
-  *bytes = flat > batch ? flat : batch;
+  size_t need = gemv_workspace_bytes(true, m, n, k);
+  const size_t batch = w4_batch_workspace_bytes(m, n, k, group_size);
+  const size_t gemm = m > kSkinnyMaxM && k <= kGemmMaxK ? w4_gemm_workspace_bytes(m, n, k) : 0;
+  if (batch > need) need = batch;
+  if (gemm > need) need = gemm;
+  *bytes = need;
   return WQ_OK;
 }
 
@@ -127,7 +132,8 @@ extern "C" int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const vo
     return WQ_OK;
   }
   return launch_w4_gemm(xh, (int)m, (int)k, reinterpret_cast<const uint4_t*>(tiles),
-                        reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream));
+                        reinterpret_cast<const uint8_t*>(meta), (int)n, (int)group_size, yh, as_stream(stream),
+                        workspace, workspace_bytes);
 }
 
 namespace {
@@ -324,7 +330,7 @@ extern "C" int wq_w8a16_linear_tiled(const uint16_t* x, int64_t m, int64_t k, co
 // itself to a kernel: the name is only a host-side handle, so every use
 // goes through the device address that hipGetSymbolAddress returns for the
 // current device, kept in g_scratch_ptr.  The largest split plan (511 tiles x
-// 4 splits x 1 KiB plus 2 KiB of counters) needs 2.0 MiB.
+// 4 splits x 1 KiB plus 16 KiB of counters) needs 2.0 MiB.
 namespace wq {
 constexpr size_t kNoAllocScratchBytes = 4u << 20;
 }  // namespace wq
@@ -394,10 +400,13 @@ extern "C" int wq_w4a16_linear_noalloc(const uint16_t* x, int64_t m, int64_t k, 
   if (int st = linear_shape_check(m, n, k)) return st;
   if (m == 0) return wq_w4a16_linear(x, m, k, tiles, meta, n, group_size, y, nullptr, 0, stream);
   size_t need = gemv_workspace_bytes(true, m, n, k);
-  // The small-batch kernel's partials (5 <= m <= 32) when they fit; beyond
-  // that the linear runs the skinny kernels, which need no scratch.
+  // The small-batch kernel's (12 <= m <= 32) and the deep-ring GEMM's split
+  // partials when they fit; beyond that the linear runs without the split
+  // (skinny kernels, or the deep ring over the whole k range).
   const size_t batch = w4_batch_workspace_bytes(m, n, k, group_size);
   if (batch > need && batch <= kNoAllocScratchBytes) need = batch;
+  const size_t gemm = m > kSkinnyMaxM && k <= kGemmMaxK ? w4_gemm_workspace_bytes(m, n, k) : 0;
+  if (gemm > need && gemm <= kNoAllocScratchBytes) need = gemm;
   WQ_REQUIRE(need <= kNoAllocScratchBytes, WQ_ERR_WORKSPACE,
              "wq_w4a16_linear_noalloc: m=%lld n=%lld k=%lld needs %zu scratch bytes, more than the %zu it holds",
              (long long)m, (long long)n, (long long)k, need, kNoAllocScratchBytes);

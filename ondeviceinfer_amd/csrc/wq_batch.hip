@@ -21,7 +21,8 @@
 // With S > 1 splits the S workgroups of a tile group meet through the
 // workspace: each publishes its fp32 partials with device-coherent stores,
 // counts in with a device-scope atomic, and the last to arrive adds the S
-// partials in split order (independent of arrival order) and stores y.
+// partials in split order (independent of arrival order) and stores y.  The
+// counters sit in the workspace's fixed counter region (kSplitCounterBytes).
 #include "wq_common.h"
 #include "wq_status.h"
 
@@ -34,7 +35,8 @@ constexpr int kBatchWaves = 8;                         // waves (tiles) per work
 // there this kernel's 1088 workgroups at M = 32 took 46 us against 37.
 constexpr int kBatchMaxTiles = 1152;
 constexpr int kBatchMaxGroups = kBatchMaxTiles / kBatchWaves;
-constexpr size_t kBatchCounterBytes = 256 * ((4 * kBatchMaxGroups + 255) / 256);
+constexpr size_t kBatchCounterBytes = kSplitCounterBytes;
+static_assert(kBatchMaxGroups <= kSplitMaxCounters, "one counter per tile group");
 // Below 12 rows the skinny kernels stay ahead: the k split's publish, count
 // and sum steps cost about 3 us per launch, more than the shared x saves
 // there (MI355X, fused QKV 5120->7168: M = 8 9.9 against 9.1 us; M = 16

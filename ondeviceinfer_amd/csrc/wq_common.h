@@ -84,6 +84,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int
 
 constexpr int kNtPolicy = 2;   // non-temporal: data streamed once
 
+// Workspace layout shared by every kernel that splits a tile's k range over
+// workgroups (decode GEMV, small-batch kernel, deep-ring GEMM): uint32
+// arrival counters in this fixed region at the start, then that kernel's
+// fp32 partials.  Every call leaves the counters it used at zero, and no
+// kernel's partials reach into the region, so one buffer can serve all the
+// kernels and shapes in turn.
+constexpr size_t kSplitCounterBytes = 16384;
+constexpr int kSplitMaxCounters = (int)(kSplitCounterBytes / 4);
+
 // 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane L's
 // bytes land at lds_base + 16 * L (out-of-range offsets land as zeros).
 // Kept out of kernel templates: with the builtin written inside one, the

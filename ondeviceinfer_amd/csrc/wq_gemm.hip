@@ -370,24 +370,40 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// With gridDim.z = S > 1 (W4, small grids) the K/128 blocks are split in S
+// ranges, one per z: each workgroup publishes its fp32 partial tile through
+// the workspace (device-coherent stores, then a device-scope arrival count on
+// its (bx, by) tile) and the last to arrive adds the S partials in split
+// order and stores y, so the result does not depend on arrival order.  The
+// counters sit in a fixed region at the start of the workspace and are back
+// at zero after every call.
+constexpr int kDeepMaxTiles = kSplitMaxCounters;          // (bx, by) tiles with a counter
+constexpr size_t kDeepCounterBytes = kSplitCounterBytes;
+
 template <GFmt F, int NT, int MT, int D>
 __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restrict__ x, int M, int K,
                                                            const void* __restrict__ wsrc,
                                                            const void* __restrict__ wmeta, int N, int bpg,
                                                            const half_t* __restrict__ bias, half_t* __restrict__ y,
-                                                           int rpx, int w8_tiled) {
+                                                           int rpx, int w8_tiled, float4_t* ws_part,
+                                                           uint32_t* ws_cnt) {
   constexpr int BM = MT * 16;
   constexpr int kStageBytes = BM * kRowBytes;
   constexpr int kInstrPerWave = BM * 16 / 64 / 4;   // 1 KiB direct loads per wave per stage
   constexpr int kLoadsPerBlock = kInstrPerWave + (F == GFmt::W4 ? 3 : 2) * NT;
   static_assert(D >= 3 && (D - 2) * kLoadsPerBlock <= 63, "ring depth");
   __shared__ __attribute__((aligned(1024))) uint8_t xs[D * kStageBytes];
+  __shared__ uint32_t arrival;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 15, kb = lane >> 4;
   const int ntile = (N + 15) >> 4;
   const int nblk = K / kW4BlockK;
+  // This workgroup's k range [b_lo, b_lo + nloc) of the S splits; block
+  // indices below are relative to b_lo.
+  const int S = gridDim.z, split = blockIdx.z;
+  const int b_lo = (split * nblk) / S, nloc = ((split + 1) * nblk) / S - b_lo;
   int bx, by;
   gemm_coords(rpx, bx, by);
   const int m0 = by * BM;
@@ -404,9 +420,9 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
   const half_t* xw = x + (size_t)m0 * K;
   const int64_t x_bytes = (int64_t)(M - m0) * K * 2;
   auto copy_x = [&](int blk, int st) {
-    // Blocks past the end (the ring's tail) read nothing: an empty range.
-    const __amdgpu_buffer_rsrc_t r =
-        buf_rsrc(xw + (size_t)blk * kW4BlockK, blk < nblk ? x_bytes - (int64_t)blk * kRowBytes : 0);
+    // Blocks past the range (the ring's tail) read nothing: an empty range.
+    const __amdgpu_buffer_rsrc_t r = buf_rsrc(xw + (size_t)(b_lo + blk) * kW4BlockK,
+                                              blk < nloc ? x_bytes - (int64_t)(b_lo + blk) * kRowBytes : 0);
 #pragma unroll
     for (int j = 0; j < kInstrPerWave; ++j) {
       const int J = wave * kInstrPerWave + j;
@@ -430,8 +446,9 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
   // Blocks past the end take an offset beyond every buffer's range, so they
   // read zeros without touching memory.
   constexpr uint32_t kPastEnd = 0x80000000u;
-  auto fetch_w = [&](int blk, WRegs<F, NT>& r) {
-    const bool live = blk < nblk;
+  auto fetch_w = [&](int lblk, WRegs<F, NT>& r) {
+    const bool live = lblk < nloc;
+    const int blk = b_lo + lblk;
     if constexpr (F == GFmt::W4) {
       const int ngrp = nblk / bpg, g = blk / bpg;
 #pragma unroll
@@ -483,14 +500,45 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
       copy_x(base + u + D - 1, (u + D - 1) % D);
       fetch_w(base + u + D - 1, wr[(u + D - 1) % D]);
       __builtin_amdgcn_sched_barrier(0);
-      if (base + u < nblk) gemm_block<F, NT, MT>(xs + u * kStageBytes, wr[u], i, kb, acc);
+      if (base + u < nloc) gemm_block<F, NT, MT>(xs + u * kStageBytes, wr[u], i, kb, acc);
       wait_vmcnt<(D - 2) * kLoadsPerBlock>();
       __builtin_amdgcn_s_barrier();
     }
     base += D;
-  } while (base < nblk);
+  } while (base < nloc);
   wait_vmcnt<0>();   // the tail's empty loads, before the waves end
 
+  if (S > 1) {
+    // Partial (tile, split, wave, t, mt) at 1 KiB granules, lane l at +16l.
+    const int tile_id = by * (int)gridDim.x + bx;
+    auto part_off = [&](int s2, int t, int mt) {
+      return (uint32_t)((((((size_t)tile_id * S + s2) * 4 + wave) * NT + t) * MT + mt) * 1024 + lane * 16);
+    };
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        coherent_store16(ws_part, part_off(split, t, mt), __builtin_bit_cast(uint4_t, acc[t][mt]));
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's partials are acknowledged
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();    // ... and every wave's
+    if (tid == 0) arrival = __hip_atomic_fetch_add(&ws_cnt[tile_id], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrival != (uint32_t)(S - 1)) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float4_t sum = split == 0 ? acc[t][mt]
+                                  : __builtin_bit_cast(float4_t, coherent_load16(ws_part, part_off(0, t, mt)));
+        for (int s2 = 1; s2 < S; ++s2)
+          sum += s2 == split ? acc[t][mt]
+                             : __builtin_bit_cast(float4_t, coherent_load16(ws_part, part_off(s2, t, mt)));
+        acc[t][mt] = sum;
+      }
+    if (tid == 0) __hip_atomic_store(&ws_cnt[tile_id], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   gemm_store<F, NT, MT>(acc, tile0, ntile, m0, M, N, i, kb, wmeta, bias, y);
 }
 
@@ -514,13 +562,46 @@ int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, 
   return check_launch(F == GFmt::W4 ? "w4_gemm" : "w8_gemm");
 }
 
+// k splits of the deep-ring grid (W4) for grids of at most 320 workgroups:
+// enough workgroups to cover the machine several times (at most 2048 with
+// the splits) while every split keeps at least 8 blocks; 1 when the
+// workspace is missing or too small.  MI355X, µs, whole k -> split: k/v
+// (5120->1024) M = 65 / 128 / 300 22.8 / 22.5 / 23.1 -> 11.4 / 11.8 / 16.2;
+// q/o M = 65 / 128 22.9 / 27.0 -> 20.6 / 24.9; down (17408->5120) M = 65 /
+// 128 68.7 / 79.9 -> 49.0 / 59.5.  Larger grids lost: fused QKV M = 128
+// (448 workgroups) 29.2 -> 32.8, q/o M = 256 35.5 -> 37.6.
+constexpr long kDeepSplitMaxGrid = 320;
+
+template <int NT, int MT>
+int deep_splits(int M, int N, int K) {
+  const long tiles = (long)(((N + 15) / 16 + 4 * NT - 1) / (4 * NT)) * ((M + MT * 16 - 1) / (MT * 16));
+  if (tiles > kDeepSplitMaxGrid) return 1;
+  int S = 1;
+  while (S < 8 && (K / kW4BlockK) / (2 * S) >= 8 && tiles * 2 * S <= 2048) S *= 2;
+  return S;
+}
+
+template <int NT, int MT>
+size_t deep_ws_bytes(int M, int N, int K) {
+  const int S = deep_splits<NT, MT>(M, N, K);
+  if (S <= 1) return 0;
+  const size_t tiles = (size_t)(((N + 15) / 16 + 4 * NT - 1) / (4 * NT)) * ((M + MT * 16 - 1) / (MT * 16));
+  return kDeepCounterBytes + tiles * S * 4 * NT * MT * 1024;
+}
+
 template <GFmt F, int NT, int MT, int D>
 int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
-                     const half_t* bias, half_t* y, hipStream_t s, int w8_tiled) {
+                     const half_t* bias, half_t* y, hipStream_t s, int w8_tiled, void* ws = nullptr,
+                     size_t ws_bytes = 0) {
   const int ntile = (N + 15) / 16;
-  const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)));
+  int S = 1;
+  if (F == GFmt::W4 && bias == nullptr && ws != nullptr && ws_bytes >= deep_ws_bytes<NT, MT>(M, N, K))
+    S = deep_splits<NT, MT>(M, N, K);
+  const dim3 grid((unsigned)((ntile + 4 * NT - 1) / (4 * NT)), (unsigned)((M + MT * 16 - 1) / (MT * 16)),
+                  (unsigned)S);
+  float4_t* part = S > 1 ? reinterpret_cast<float4_t*>(reinterpret_cast<uint8_t*>(ws) + kDeepCounterBytes) : nullptr;
   hipLaunchKernelGGL((wq_gemm_deep_kernel<F, NT, MT, D>), grid, dim3(256), 0, s, x, M, K, w, meta, N, bpg, bias, y,
-                     xcd_rows<F>(M, grid.y), w8_tiled);
+                     xcd_rows<F>(M, grid.y), w8_tiled, part, reinterpret_cast<uint32_t*>(ws));
   return check_launch(F == GFmt::W4 ? "w4_gemm_deep" : "w8_gemm_deep");
 }
 
@@ -535,9 +616,18 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
 // M = 2048 190 -> 159 us, k_proj at M = 512 48 -> 22 us); row-major INT8,
 // whose weight loads are 16 rows x 64 B, loses from two tiles per wave and
 // keeps 64-wide slices of 64-row (M <= 256) or 128-row tiles.
+// Whether launch_gemm_auto runs the deep ring on 32-row tiles for this shape.
+bool gemm_takes_deep(long M, long N, bool w4_or_tiles) {
+  const long ntile = (N + 15) / 16, mblk = (M + 127) / 128, mb64 = (M + 63) / 64;
+  if (((ntile + 15) / 16) * mblk >= 512 || !w4_or_tiles) return false;
+  constexpr long kMinGrid = 384;
+  return ((ntile + 7) / 8) * mb64 < kMinGrid && ((ntile + 3) / 4) * mb64 < kMinGrid;
+}
+
 template <GFmt F>
 int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* meta, int N, int bpg,
-                     const half_t* bias, half_t* y, hipStream_t s, int w8_tiled) {
+                     const half_t* bias, half_t* y, hipStream_t s, int w8_tiled, void* ws = nullptr,
+                     size_t ws_bytes = 0) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128;
   if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
   if (F == GFmt::W4 || w8_tiled) {
@@ -547,7 +637,7 @@ int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* m
       return launch_gemm<F, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
     if (((ntile + 3) / 4) * mb64 >= kMinGrid)
       return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
-    return launch_gemm_deep<F, 1, 2, 6>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
+    return launch_gemm_deep<F, 1, 2, 6>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled, ws, ws_bytes);
   } else {
     if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
     return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
@@ -557,8 +647,15 @@ int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* m
 }  // namespace
 
 int launch_w4_gemm(const half_t* x, int M, int K, const uint4_t* tiles, const uint8_t* meta, int N, int G, half_t* y,
-                   hipStream_t s) {
-  return launch_gemm_auto<GFmt::W4>(x, M, K, tiles, meta, N, G / kW4BlockK, nullptr, y, s, 0);
+                   hipStream_t s, void* ws, size_t ws_bytes) {
+  return launch_gemm_auto<GFmt::W4>(x, M, K, tiles, meta, N, G / kW4BlockK, nullptr, y, s, 0, ws, ws_bytes);
+}
+
+// Workspace the W4 GEMM can use at this shape: the deep ring's k splits on
+// the smallest grids (0 when the shape takes another grid).
+size_t w4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K < kW4BlockK || !gemm_takes_deep(M, N, true)) return 0;
+  return deep_ws_bytes<1, 2>((int)M, (int)N, (int)K);
 }
 
 // The grid launch_gemm_auto picks for a W4 (or INT8-tile) shape, when it is a wq_gemm_kernel

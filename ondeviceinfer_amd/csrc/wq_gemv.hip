@@ -847,8 +847,8 @@ constexpr int kFlatSplitMaxTiles = 512;   // only shapes with fewer tiles split 
 // counter region does not depend on the shape, so one buffer shared by
 // several shapes (the allocation-free entry point's scratch) never has one
 // shape's partials written over another shape's counters.
-constexpr size_t kFlatCounterBytes = 4 * kFlatSplitMaxTiles;
-static_assert(kFlatCounterBytes % 256 == 0, "partials start 256-byte aligned");
+constexpr size_t kFlatCounterBytes = kSplitCounterBytes;
+static_assert(kFlatSplitMaxTiles <= kSplitMaxCounters, "one counter per split tile");
 
 template <WFmt F>
 FlatPlan plan_flat(int ntile, int nblk, bool may_split = true) {

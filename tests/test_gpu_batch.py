@@ -119,3 +119,60 @@ def test_batch_kernel_is_bitwise_repeatable_and_graph_safe(gpu):
             assert torch.equal(o, e), f'replay {rep}'
         backend, layer, name, xd = cases[0]
         assert torch.equal(backend.linear(xd, layer, name), eager[0])   # eager call between replays
+
+
+# ------------------------------------------------------------------ deep-ring GEMM k split
+
+@pytest.mark.parametrize('n,k', [(7168, 5120), (5120, 5120), (1024, 5120), (5120, 17408), (1000, 2048)])
+def test_deep_ring_split_matches_oracle(gpu, n, k):
+    """The smallest prefill grids (deep ring on 32-row tiles) split their k
+    range over workgroups when a workspace is given: every output against
+    the oracle, 20 repeats bit for bit, the counters back at zero, and the
+    no-workspace form (whole k range per workgroup) also within the bar."""
+    name = 'self_attn.q_proj.weight'
+    weights, x = synth.w4_case(n, k, 300, seed=70 + n % 11, name=name)
+    layer = {key: dev(v, gpu) for key, v in weights.items()}
+    backend = wq.CompressedLinearBackend('marlin')
+    backend.prepare(layer, name)
+    prep = layer['self_attn.q_proj._prepared']
+    w32 = qdq.decode_weight(weights, name).astype(np.float32)
+    for m in (65, 128, 300):
+        need = _native.w4a16_workspace_size(m, n, k, 128)
+        xd = dev(x[:m], gpu)
+        expected = (x[:m].astype(np.float32) @ w32.T).astype(np.float16)
+        if need == 0:
+            check_parity(host(backend.linear(xd, layer, name)), expected, f'deep n={n} k={k} m={m} (no split)')
+            continue
+        ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+        first = _native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128, workspace=ws).clone()
+        check_parity(host(first), expected, f'deep split n={n} k={k} m={m}')
+        for _ in range(20):
+            assert torch.equal(_native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128, workspace=ws), first)
+        assert torch.count_nonzero(ws[:16384]).item() == 0
+        tiny = torch.zeros(16, dtype=torch.uint8, device=gpu)
+        whole = host(_native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128, workspace=tiny))
+        check_parity(whole, expected, f'deep whole-k n={n} k={k} m={m}')
+
+
+def test_split_kernels_share_one_workspace(gpu):
+    """One buffer serving the decode GEMV's split (m = 1, 17408 -> 5120), the
+    small-batch kernel (m = 24) and the deep-ring split (m = 128), called in
+    turn twice: each result equals its own-workspace call bit for bit."""
+    cases = []
+    for i, (n, k, m) in enumerate(((5120, 17408, 1), (7168, 5120, 24), (7168, 5120, 128), (1024, 5120, 96))):
+        name = 'mlp.down_proj.weight'
+        weights, x = synth.w4_case(n, k, m, seed=90 + i, name=name)
+        layer = {key: dev(v, gpu) for key, v in weights.items()}
+        wq.CompressedLinearBackend('marlin').prepare(layer, name)
+        prep = layer['mlp.down_proj._prepared']
+        xd = dev(x, gpu)
+        own = torch.zeros(max(_native.w4a16_workspace_size(m, n, k, 128), 16), dtype=torch.uint8, device=gpu)
+        ref = _native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128, workspace=own).clone()
+        cases.append((n, k, m, prep, xd, ref))
+    need = max(_native.w4a16_workspace_size(m, n, k, 128) for n, k, m, *_ in cases)
+    assert need > 0
+    shared = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    for rep in range(2):
+        for n, k, m, prep, xd, ref in cases:
+            got = _native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128, workspace=shared)
+            assert torch.equal(got, ref), f'n={n} k={k} m={m} call {rep}'

@@ -237,19 +237,28 @@ def test_w4a16_prefill_full_shapes_sampled_rows(gpu, k, n):
 
 @pytest.mark.parametrize('k,n', [(5120, 1024), (17408, 5120), (5120, 7168)])
 def test_w4a16_prefill_grids_agree_across_m(gpu, k, n):
-    """Every prefill-GEMM grid (128- or 64-wide n slices of 128-, 64- or
-    32-row tiles, plain or deep ring, chosen by the grid size; from 4096 rows
-    on, row blocks owned per XCD) sums each output in the same order, so the
-    rows of an M-row call equal the same rows of a 4096-row call bit for bit;
-    48 rows of the 4096-row call against the oracle."""
+    """Every prefill-GEMM grid that keeps each tile's k range in one
+    workgroup (128- or 64-wide n slices of 128-, 64- or 32-row tiles, plain
+    or deep ring, chosen by the grid size; from 4096 rows on, row blocks owned
+    per XCD) sums each output in the same order, so the rows of an M-row call
+    equal the same rows of a 4096-row call bit for bit.  The smallest grids
+    split the deep ring's k range when a workspace is given (their rows then
+    differ by the fp32 summation order): those calls are checked against the
+    oracle, and their no-workspace form bit for bit.  48 rows of the
+    4096-row call against the oracle."""
     name = 'mlp.up_proj.weight'
     weights, _ = synth.w4_case(n, k, 1, seed=5, name=name)
     x = np.random.default_rng(6).standard_normal((4096, k), dtype=np.float32).astype(np.float16)
     backend, layer = prepared_w4(weights, name, gpu)
+    prep = layer['mlp.up_proj._prepared']
     xd = dev(x, gpu)
     y_full = host(backend.linear(xd, layer, name))
+    tiny = torch.zeros(16, dtype=torch.uint8, device=gpu)
     for m in (65, 96, 128, 300, 512, 1024, 2048):
         y = host(backend.linear(xd[:m], layer, name))
+        if _native.w4a16_workspace_size(m, n, k, 128) > 0:
+            check_parity(y, qdq.qdq_linear(x[:m], weights, name), f'w4 prefill split {k}->{n} m={m}')
+            y = host(_native.w4a16_linear(xd[:m], prep.tiles, prep.meta, n, 128, workspace=tiny))
         assert np.array_equal(bits(y), bits(y_full[:m])), f'{k}->{n} m={m} differs from the 4096-row call'
     rows = np.sort(np.random.default_rng(7).choice(4096, size=48, replace=False))
     check_parity(y_full[rows], qdq.qdq_linear(x[rows], weights, name), f'w4 prefill {k}->{n} m=4096 rows')
