@@ -120,21 +120,17 @@ int wq_w4a16_linear(const uint16_t* x, int64_t m, int64_t k, const void* tiles, 
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* wq_w4a16_linear without a workspace argument and without any allocation:
- * the k-split counters and partials live in a fixed 4 MiB
- * device array inside the library (one per GPU, held until the process
- * ends), so the call is as fast as wq_w4a16_linear with its workspace.
+ * the k-split counters and partials live in a fixed 16 MiB device array
+ * inside the library (one per GPU, held until the process ends), so the call
+ * runs the same plan, with the same results, as wq_w4a16_linear with a
+ * workspace of wq_w4a16_workspace_size bytes (every split plan fits 16 MiB).
  * Every call on a GPU shares that GPU's array: calls that may overlap on one
  * GPU (different streams, or graphs replayed concurrently) race and must be
  * ordered by the caller.  The first call on a device looks the array up
  * (hipGetSymbolAddress) and queues a clear of it on `stream`; that first call
  * must not be under stream capture (it returns WQ_ERR_UNSUPPORTED there, so
  * no clear is ever recorded into a graph): make one eager call per device
- * before capturing later ones, which then record only the linear.  Decode
- * shapes (m <= 4) whose split plan would need more than 4 MiB return
- * WQ_ERR_WORKSPACE (none of the planner's current shapes do: its largest
- * split needs 2 MiB); a small-batch plan (12 <= m <= 32) or a deep-ring GEMM
- * split (the smallest prefill grids) that does not fit runs without the split
- * instead, as wq_w4a16_linear does with a short workspace.
+ * before capturing later ones, which then record only the linear.
  * No counterpart in the reference: it exists for callers that cannot
  * allocate (code under HIP graph capture, serving loops and harnesses that
  * forbid hipMalloc). */

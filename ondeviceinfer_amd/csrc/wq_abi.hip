@@ -324,15 +324,17 @@ extern "C" int wq_w8a16_linear_tiled(const uint16_t* x, int64_t m, int64_t k, co
 // ---------------------------------------------------------------------------
 // Allocation-free W4A16 linear (wq_w4a16_linear_noalloc).
 //
-// The decode GEMV's k-split counters and fp32 partials live in this
-// file-scope device array instead of a caller workspace.  Each GPU holds its
-// own copy for the life of the process.  Host code never passes `scratch`
-// itself to a kernel: the name is only a host-side handle, so every use
-// goes through the device address that hipGetSymbolAddress returns for the
-// current device, kept in g_scratch_ptr.  The largest split plan (511 tiles x
-// 4 splits x 1 KiB plus 16 KiB of counters) needs 2.0 MiB.
+// The k-split counters and fp32 partials of the split kernels (decode GEMV,
+// small-batch kernel, deep-ring GEMM) live in this file-scope device array
+// instead of a caller workspace.  Each GPU holds its own copy for the life of
+// the process.  Host code never passes `scratch` itself to a kernel: the name
+// is only a host-side handle, so every use goes through the device address
+// that hipGetSymbolAddress returns for the current device, kept in
+// g_scratch_ptr.  Every split plan fits its 16 MiB (kSplitWorkspaceMaxBytes:
+// plans that would need more take fewer splits), e.g. the decode GEMV's
+// largest 2.0 MiB, the deep ring's up to 16 MiB.
 namespace wq {
-constexpr size_t kNoAllocScratchBytes = 4u << 20;
+constexpr size_t kNoAllocScratchBytes = kSplitWorkspaceMaxBytes;
 }  // namespace wq
 
 static __device__ __align__(256) uint8_t scratch[wq::kNoAllocScratchBytes];
@@ -399,14 +401,11 @@ extern "C" int wq_w4a16_linear_noalloc(const uint16_t* x, int64_t m, int64_t k, 
                                        int64_t n, int64_t group_size, uint16_t* y, void* stream) {
   if (int st = linear_shape_check(m, n, k)) return st;
   if (m == 0) return wq_w4a16_linear(x, m, k, tiles, meta, n, group_size, y, nullptr, 0, stream);
-  size_t need = gemv_workspace_bytes(true, m, n, k);
-  // The small-batch kernel's (12 <= m <= 32) and the deep-ring GEMM's split
-  // partials when they fit; beyond that the linear runs without the split
-  // (skinny kernels, or the deep ring over the whole k range).
-  const size_t batch = w4_batch_workspace_bytes(m, n, k, group_size);
-  if (batch > need && batch <= kNoAllocScratchBytes) need = batch;
-  const size_t gemm = m > kSkinnyMaxM && k <= kGemmMaxK ? w4_gemm_workspace_bytes(m, n, k) : 0;
-  if (gemm > need && gemm <= kNoAllocScratchBytes) need = gemm;
+  // The same sizing as wq_w4a16_workspace_size: every split plan (decode
+  // GEMV, small-batch kernel, deep-ring GEMM) fits kSplitWorkspaceMaxBytes,
+  // so this runs the plan a caller workspace would.
+  size_t need = 0;
+  if (int st = wq_w4a16_workspace_size(m, n, k, group_size, &need)) return st;
   WQ_REQUIRE(need <= kNoAllocScratchBytes, WQ_ERR_WORKSPACE,
              "wq_w4a16_linear_noalloc: m=%lld n=%lld k=%lld needs %zu scratch bytes, more than the %zu it holds",
              (long long)m, (long long)n, (long long)k, need, kNoAllocScratchBytes);

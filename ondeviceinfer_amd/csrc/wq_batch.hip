@@ -262,6 +262,8 @@ BatchPlan batch_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
     const int s = (int)(nblk / r);
     if (s > 16) continue;
     if ((r * p.mc * 4) % kBatchWaves != 0) continue;
+    if (s > 1 && kBatchCounterBytes + (size_t)p.groups * s * kBatchWaves * p.mc * 1024 > kSplitWorkspaceMaxBytes)
+      continue;
     p.r = r;
     p.s = s;
     return p;

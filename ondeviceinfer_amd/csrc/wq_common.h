@@ -92,6 +92,11 @@ constexpr int kNtPolicy = 2;   // non-temporal: data streamed once
 // kernels and shapes in turn.
 constexpr size_t kSplitCounterBytes = 16384;
 constexpr int kSplitMaxCounters = (int)(kSplitCounterBytes / 4);
+// Largest workspace any split plan asks for (counters + partials): plans
+// that would need more take fewer splits, so the allocation-free entry
+// point's fixed scratch of this size runs the same plan as a caller
+// workspace.
+constexpr size_t kSplitWorkspaceMaxBytes = 16u << 20;
 
 // 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane L's
 // bytes land at lds_base + 16 * L (out-of-range offsets land as zeros).

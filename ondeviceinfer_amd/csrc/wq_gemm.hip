@@ -577,7 +577,9 @@ int deep_splits(int M, int N, int K) {
   const long tiles = (long)(((N + 15) / 16 + 4 * NT - 1) / (4 * NT)) * ((M + MT * 16 - 1) / (MT * 16));
   if (tiles > kDeepSplitMaxGrid) return 1;
   int S = 1;
-  while (S < 8 && (K / kW4BlockK) / (2 * S) >= 8 && tiles * 2 * S <= 2048) S *= 2;
+  while (S < 8 && (K / kW4BlockK) / (2 * S) >= 8 && tiles * 2 * S <= 2048 &&
+         kDeepCounterBytes + (size_t)tiles * 2 * S * 4 * NT * MT * 1024 <= kSplitWorkspaceMaxBytes)
+    S *= 2;
   return S;
 }
 
