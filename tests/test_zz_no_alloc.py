@@ -45,18 +45,19 @@ def _noalloc(x, p, n):
 
 
 def test_noalloc_matches_workspace_entry_point(gpu):
-    # (n, k, m): the first two use the k-split scratch (320 and 64 tiles,
-    # 4 splits), the second smaller than the first; then a non-split decode
-    # shape, a skinny M and a GEMM M, which use no scratch.
+    # (n, k, m): the first two use the decode GEMV's k-split scratch (320 and
+    # 64 tiles, 4 splits), the second smaller than the first; then a non-split
+    # decode shape and a skinny M, which use no scratch; a GEMM M on the deep
+    # ring's k split and a small-batch M, which use it again.
     cases = [(5120, 17408, 1), (1024, 8448, 1), (1024, 8448, 4), (5120, 5120, 1), (1024, 8448, 33),
-             (1024, 8448, 100)]
+             (1024, 8448, 100), (7168, 5120, 24)]
     gen = torch.Generator(device=gpu).manual_seed(0)
     for idx, (n, k, m) in enumerate(cases):
         print(f'noalloc case {idx}: n={n} k={k} m={m}', flush=True)
         p = _prepared(n, k, idx, gpu)
         x = torch.randn(m, k, generator=gen, device=gpu).half()
         expected, ws_bytes = _with_workspace(x, p, n)
-        if idx < 3:
+        if idx < 3 or idx >= 5:
             assert ws_bytes > 0   # these shapes exercise the scratch
         got = _noalloc(x, p, n)
         torch.cuda.synchronize()
