@@ -21,10 +21,15 @@ Also in the same JSON line:
   (q, k, v, o, gate, up, down x 40 layers) replayed as one graph; GB/s of
   algorithmic bytes ``N*K/2 + N*(K/128)*2.5 + 2MK + 2MN``;
 * ``roofline``: the dominant kernel of the decode step (largest time per
-  token), its algorithmic bytes per launch / its average launch time measured
-  here with HIP events around a graph of that kernel's launches on the stream
-  they run on; ``traffic`` from the committed rocprofv3 counter summary;
-* ``decode_step_kernels``: the same timing for every kernel of the step;
+  token), its algorithmic bytes per launch / its average launch duration
+  inside the decode step (torch.profiler device records over 16 decode steps
+  run right after the timed ones, on the same model and cache);
+  ``one_op_graph_us`` is the same kernel timed in a graph of only its own
+  launches; ``traffic`` from the committed rocprofv3 counter summary;
+* ``decode_step_kernels``: every kernel of the step, each timed in a graph of
+  its own launches (``kernel_us``: device records; ``us_per_launch``: HIP
+  events, launch gaps included) and, for the step's kernels, inside the
+  step (``in_step_us``);
 * ``prefill``: the M=4096 W4A16 GEMM per shape, TFLOP/s, next
   to the vendor library's dense fp16 GEMM (torch.matmul -> hipBLASLt, no
   dequantization) on the same shape for context;
@@ -68,6 +73,7 @@ PUBLISHED_TOKS = 26.358          # AWQ INT4 G=128 + vLLM Marlin, RT
 # Peak allocated GiB the reference publishes for the same runs (README.md:31-32).
 REFERENCE_PEAK_GIB = {'w4': 9.260, 'int8': 15.517}
 HBM_PEAK_GBS = 8000.0
+PROFILED_STEPS = 16   # decode steps after the timed ones, under torch.profiler, for in-step kernel durations
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 INT8_MFMA_PEAK_TOPS = 5000.0      # dense int8 MFMA, MI355X
 GROUP = 128
@@ -136,6 +142,54 @@ def kernel_us(torch, graph, reps: int, launches: int, event_us: float) -> tuple[
     if kt and abs(seen - launches) < 0.5 and 0.5 * event_us <= kus <= 1.1 * event_us:
         return kus, 'kernel'
     return event_us, 'events'
+
+
+def step_kernel_times(torch, model, token, cache, steps: int) -> dict:
+    """Average device duration (µs) and launches per step of each kernel of
+    the decode step, from torch.profiler's device records over `steps`
+    decode steps run right after the timed ones on the same model and cache
+    (the kernels as the step interleaves them, which is what rocprofv3's
+    kernel trace of the timed steps shows)."""
+    from collections import defaultdict
+    from torch.profiler import ProfilerActivity, profile
+    from ondeviceinfer_amd.generation import greedy_token
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        for _ in range(steps):
+            token = greedy_token(model(token, cache=cache, logits_to_keep=1))
+        torch.cuda.synchronize()
+    per = defaultdict(list)
+    for e in prof.events():
+        if e.device_type == torch.autograd.DeviceType.CUDA:
+            per[e.name].append(e.device_time)
+    return {name: {'us': sum(v) / len(v), 'per_step': len(v) / steps} for name, v in per.items()}
+
+
+def step_record_pattern(kernel: str) -> str | None:
+    """The mangled-name fragment of a decode-step kernel named as in the
+    report (``gemv_flat_kernel<10, 1, W4, RmsNorm>``), as the profiler's
+    device records carry it; None for names without one."""
+    import re
+    m = re.fullmatch(r'gemv_flat_kernel<(\d+), (\d+), (W4|W8)(?:, (RmsNorm|SiluMul))?>', kernel)
+    if not m:
+        return None
+    fmt = {'W4': 0, 'W8': 1}[m.group(3)]
+    mode = {None: 0, 'RmsNorm': 1, 'SiluMul': 2}[m.group(4)]
+    return f'gemv_flat_kernelILi{m.group(1)}ELi{m.group(2)}ELNS0_4WFmtE{fmt}ELNS0_5XModeE{mode}E'
+
+
+def in_step_us(step_times: dict, patterns: tuple, launches_per_step: int) -> float | None:
+    """Summed per-launch device time of the kernels whose records contain
+    each of `patterns` (one kernel per pattern, each launched
+    `launches_per_step` times per step), or None when any is missing or
+    launched a different number of times."""
+    total = 0.0
+    for pat in patterns:
+        hits = [v for name, v in step_times.items() if pat in name]
+        if len(hits) != 1 or abs(hits[0]['per_step'] - launches_per_step) > 0.01:
+            return None
+        total += hits[0]['us']
+    return total
 
 
 def time_graph(torch, graph, reps: int) -> float:
@@ -428,12 +482,14 @@ def build_model(torch, layers: int, device, keep_raw: tuple = ()):
     return cfg, model, runtime, setup, raw
 
 
-def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: int, result: dict) -> None:
+def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: int, result: dict,
+                    step_times: dict | None) -> None:
     """The measurement sections beside the headline: the configs[1] GEMV pass,
     the decode step's kernels (roofline), the M=4096 prefill GEMMs and
     attention, the configs[3] batch sweep, the INT8 kernels and the copy
-    ceiling; each adds its key to `result`.  Its buffers are locals, freed
-    on return."""
+    ceiling; each adds its key to `result`.  `step_times` (step_kernel_times
+    of the headline model) gives each decode-step kernel's duration inside
+    the step.  Its buffers are locals, freed on return."""
     layers = [runtime.weights_for(i) for i in range(args.layers)]
     outs, xs = {}, {k: torch.randn(1, k, device=device).half() for k in (HIDDEN, INTER)}
 
@@ -578,16 +634,37 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
     del g
     for e in kernels:
         e['us_per_token'] = round(e['kernel_us'] * e['launches_per_token'], 2)
+        if not e['in_decode_step']:
+            continue
+        # The same kernel inside the decode steps (profiled after the timed ones).
+        if e['op'] == 'attention':
+            pats = ('decode_attention_kernel', 'decode_attention_merge_kernel')
+        elif e['op'] == 'lm_head':
+            pats = ('lm_head_kernel', 'lm_head_pick_kernel')
+        else:
+            pats = (step_record_pattern(e['kernel']),)
+        us = in_step_us(step_times, pats, e['launches_per_token']) if step_times and all(pats) else None
+        if us is not None:
+            e['in_step_us'] = round(us, 3)
+            e['in_step_frac'] = round(e['bytes'] / us / 1e3 / HBM_PEAK_GBS, 4)
     step = [e for e in kernels if e['in_decode_step']]
     dom = max(step, key=lambda e: e['us_per_token'])
     # achieved = algorithmic bytes per launch / the kernel's own average
-    # duration (torch.profiler device records, as rocprofv3 reports it);
-    # graph_us_per_launch adds the launch gaps of back-to-back replays.
+    # duration in the decode steps (torch.profiler device records, as
+    # rocprofv3's kernel trace reports it); one_op_graph_us is the same
+    # kernel in a graph of only its own launches (one per layer), and
+    # graph_us_per_launch adds that graph's launch gaps.
+    if 'in_step_us' in dom:
+        avg_us, timing = dom['in_step_us'], f'kernel: device records over {PROFILED_STEPS} decode steps'
+    else:
+        avg_us, timing = dom['kernel_us'], dom['timing'] + ': one-op graph'
+    achieved = dom['bytes'] / avg_us / 1e3
     result['roofline'] = {
-        'bound': 'hbm', 'achieved': dom['gbs'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': dom['frac'],
+        'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+        'frac': round(achieved / HBM_PEAK_GBS, 4),
         'traffic': profiled_traffic(dom['kernel'], dom['shape']), 'kernel': dom['kernel'], 'shape': dom['shape'],
-        'op': dom['op'], 'avg_launch_us': dom['kernel_us'], 'timing': dom['timing'],
-        'graph_us_per_launch': dom['us_per_launch'],
+        'op': dom['op'], 'avg_launch_us': round(avg_us, 3), 'timing': timing,
+        'one_op_graph_us': dom['kernel_us'], 'graph_us_per_launch': dom['us_per_launch'],
         'algorithmic_bytes_per_launch': dom['bytes'],
         # the metric's second half: the configs[1] GEMV pass, % of HBM peak
         'gemv_pass_pct_hbm_peak': result['gemv_pass']['pct_hbm_peak'],
@@ -817,10 +894,10 @@ def main() -> int:
         validation = kernel_validation(torch, raw, device)
         del raw
         torch.cuda.empty_cache()
-    capacity = PROMPT + 1 + args.warmup + args.steps
+    capacity = PROMPT + 1 + args.warmup + args.steps + PROFILED_STEPS
     prompt = torch.randint(0, cfg.vocab_size, (1, PROMPT), generator=torch.Generator().manual_seed(0)).to(device)
 
-    def generate(n_untimed: int, n_timed: int):
+    def generate(n_untimed: int, n_timed: int, n_profiled: int = 0):
         cache = model.make_resident_cache(batch_size=1, max_seq_len=capacity)
         torch.cuda.synchronize()
         # Peak allocated over prefill + decode with the cache already made,
@@ -841,7 +918,8 @@ def main() -> int:
         decode_s = time.perf_counter() - t_d
         peak = torch.cuda.max_memory_allocated(device)
         check_step(model, token, cache)
-        return prefill_s, decode_s, cache, peak
+        times = step_kernel_times(torch, model, token, cache, n_profiled) if n_profiled else None
+        return prefill_s, decode_s, cache, peak, times
 
     log('warm-up generation (captures the decode-step graph)')
     t0 = time.perf_counter()
@@ -850,8 +928,9 @@ def main() -> int:
     del cache
     generate(2, 0)
     log(f'timed generation: prefill {PROMPT}, {args.warmup} untimed + {args.steps} timed decode tokens')
-    prefill_s, decode_s, cache, peak_bytes = generate(args.warmup, args.steps)
-    assert cache.lengths[0] == PROMPT + args.warmup + args.steps + 1
+    prefill_s, decode_s, cache, peak_bytes, step_times = generate(
+        args.warmup, args.steps, 0 if args.no_extras else PROFILED_STEPS)
+    assert cache.lengths[0] == PROMPT + args.warmup + args.steps + 1 + (0 if args.no_extras else PROFILED_STEPS)
     toks = args.steps / decode_s
     weight_bytes = runtime.resident_storage_bytes
     kv_bytes_per_token = 2 * args.layers * cfg.num_key_value_heads * cfg.head_dim * 2 * (PROMPT + args.warmup)
@@ -879,7 +958,7 @@ def main() -> int:
     del cache
 
     if not args.no_extras:
-        kernel_sections(torch, native, model, runtime, cfg, args, device, capacity, result)
+        kernel_sections(torch, native, model, runtime, cfg, args, device, capacity, result, step_times)
         result['kernel_validation'] = validation
 
     if not args.no_extras:
@@ -890,7 +969,7 @@ def main() -> int:
         log('W4 LM head variant: quantize the head, capture, decode')
         model.quantize_lm_head()
         generate(2, 0)
-        _, dec_w4, cache, peak_w4 = generate(args.warmup, args.steps)
+        _, dec_w4, cache, peak_w4, _ = generate(args.warmup, args.steps)
         del cache
         tb, mb = native.w4_repack_size(cfg.vocab_size, cfg.hidden_size, GROUP)
         result['e2e_w4_lm_head'] = {
