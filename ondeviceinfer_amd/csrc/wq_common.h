@@ -76,7 +76,11 @@ __device__ __forceinline__ uint4_t coherent_load16(const void* base, uint32_t by
 }
 
 // Buffer over [base, base + bytes) (bytes clamped to the 31-bit record
-// count); accesses at or past the end read as zero.
+// count); accesses at or past the end read as zero.  The range check covers
+// the sum of the lane offset (voffset) and the wave-uniform one (soffset):
+// on MI355X a load whose soffset alone, or whose voffset + soffset, passes
+// the range returned zeros (measured with both inside one allocation), which
+// is what the kernels' past-the-end soffsets rely on.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int64_t bytes) {
   const int nrec = (int)(bytes < 0 ? 0 : bytes > 0x7fffffff ? 0x7fffffff : bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrec, kBufferRsrcWord3);

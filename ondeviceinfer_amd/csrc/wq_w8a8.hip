@@ -159,7 +159,7 @@ __device__ __forceinline__ void i8_read_frags(uint4_t (&b)[MT], uint32_t a) {
 // fragments come straight from memory into registers one stage ahead.  Per
 // 64-k step a wave reads MT x fragments from LDS and issues NT x MT int8
 // MFMAs.  Two workgroups per CU (the accumulators then live in VGPRs, not
-// AGPRs: 223 registers, no scratch), so one workgroup's load wait overlaps
+// AGPRs: 236 registers, no scratch), so one workgroup's load wait overlaps
 // the other's math: 1.4-1.8x the throughput of one per CU.  K % 128 == 0.
 template <int NT, int MT>
 __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restrict__ qx,
@@ -222,19 +222,10 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = int4v_t{0, 0, 0, 0};
 
-  uint4_t cur[NT][2], nxt[NT][2];
   const uint32_t xs_lds = (uint32_t)(size_t)((const __attribute__((address_space(3))) uint8_t*)xs);
-  copy_x(0, 0);
-  fetch_w(0, cur);
-  __builtin_amdgcn_s_waitcnt(0);   // stage 0 landed
-  __syncthreads();
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int st = blk & 1;
-    const bool more = blk + 1 < nblk;
-    if (more) {
-      copy_x(blk + 1, st ^ 1);
-      fetch_w(blk + 1, nxt);
-    }
+  // The one-tile path's block math: two 64-k MFMA steps of stage `st` with
+  // the weight registers w (the same steps as the loop of the wider grids).
+  auto block_math = [&](int st, const uint4_t (&w)[NT][2]) {
     // Row r = mt*16 + i of the stage holds chunk c at slot i8_swz(r, c) =
     // c ^ ((i >> 1) & 7): one lane address per step, mt in the offset.
     const uint32_t stage = xs_lds + (uint32_t)(st * kStageBytes + i * kI8RowBytes);
@@ -247,22 +238,101 @@ __global__ __launch_bounds__(256, 2) void w8a8_gemm_kernel(const int8_t* __restr
 #pragma unroll
       for (int mt = 0; mt < (MT + 1) / 2; ++mt)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b[mt], acc[t][mt]);
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(w[t][step], b[mt], acc[t][mt]);
       lds_wait_rest<MT>(b);
 #pragma unroll
       for (int mt = (MT + 1) / 2; mt < MT; ++mt)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b[mt], acc[t][mt]);
+        for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(w[t][step], b[mt], acc[t][mt]);
     }
-    if (more) {
+  };
+  if constexpr (NT == 1) {
+    // One weight tile per wave (grids of at most one round of workgroups):
+    // the loop is unrolled by two over two fixed register sets, every step
+    // issues its loads (the block after the last reads nothing: a
+    // past-the-end offset), and the per-block wait covers only the x copy,
+    // issued before the weights, so the next block's weights may still be in
+    // flight across the barrier (M = 512, same box, same bits: 17408->5120
+    // 116.7 -> 84.1 us, 5120^2 38.8 -> 33.7 us; M = 4096 k_proj 43.0 ->
+    // 40.2 us).  The larger grids keep the loop below: this form cost them
+    // 1-2 %.
+    constexpr uint32_t kPastEnd = 0x80000000u;
+    constexpr int kWLoads = 2 * NT;   // weight loads per block per wave
+    uint4_t wr[2][NT][2];
+    copy_x(0, 0);
+    fetch_w(0, wr[0]);
+    __builtin_amdgcn_s_waitcnt(0);   // stage 0 landed
+    __syncthreads();
+    int base = 0;
+    do {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        cur[t][0] = nxt[t][0];
-        cur[t][1] = nxt[t][1];
+      for (int u = 0; u < 2; ++u) {
+        const int blk = base + u;
+#pragma unroll
+        for (int j = 0; j < kInstrPerWave; ++j) {   // copy_x(blk + 1, u ^ 1), empty past the end
+          const int J = wave * kInstrPerWave + j;
+          const int r = 8 * J + (lane >> 3);
+          lds_load16(rx, (uint32_t)(r * K + 16 * i8_swz(r, lane & 7)),
+                     blk + 1 < nblk ? (uint32_t)((blk + 1) * kI8Blk) : kPastEnd, xs + (u ^ 1) * kStageBytes + J * 1024);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {               // fetch_w(blk + 1, wr[u ^ 1]), empty past the end
+          const uint32_t so = blk + 1 >= nblk ? kPastEnd
+                              : wl8.tiled ? (uint32_t)((t * nblk + blk + 1) * kW8TileBlockBytes)
+                                          : (uint32_t)(t * 16 * K + (blk + 1) * kI8Blk);
+          wr[u ^ 1][t][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff, so, 0);
+          wr[u ^ 1][t][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff + w_p1, so, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep the loads in this order: the wait below counts them
+        if (blk < nblk) block_math(u, wr[u]);
+        __builtin_amdgcn_s_waitcnt((kWLoads & 0xF) | ((kWLoads >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+        __builtin_amdgcn_s_barrier();   // every wave's part of stage u ^ 1 landed
       }
+      base += 2;
+    } while (base < nblk);
+    __builtin_amdgcn_s_waitcnt(0);   // the run-out block's empty loads, before the stores
+  } else {
+    uint4_t cur[NT][2], nxt[NT][2];
+    copy_x(0, 0);
+    fetch_w(0, cur);
+    __builtin_amdgcn_s_waitcnt(0);   // stage 0 landed
+    __syncthreads();
+    for (int blk = 0; blk < nblk; ++blk) {
+      const int st = blk & 1;
+      const bool more = blk + 1 < nblk;
+      if (more) {
+        copy_x(blk + 1, st ^ 1);
+        fetch_w(blk + 1, nxt);
+      }
+      // Row r = mt*16 + i of the stage holds chunk c at slot i8_swz(r, c) =
+      // c ^ ((i >> 1) & 7): one lane address per step, mt in the offset.
+      const uint32_t stage = xs_lds + (uint32_t)(st * kStageBytes + i * kI8RowBytes);
+#pragma unroll
+      for (int step = 0; step < 2; ++step) {
+        const int c = 4 * step + kb;   // 16-byte chunk of this lane's k range
+        uint4_t b[MT];
+        i8_read_frags<MT>(b, stage + (uint32_t)(i8_swz(i, c) * 16));
+        lds_wait_first_half<MT>(b);
+#pragma unroll
+        for (int mt = 0; mt < (MT + 1) / 2; ++mt)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b[mt], acc[t][mt]);
+        lds_wait_rest<MT>(b);
+#pragma unroll
+        for (int mt = (MT + 1) / 2; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_i8(cur[t][step], b[mt], acc[t][mt]);
+      }
+      if (more) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          cur[t][0] = nxt[t][0];
+          cur[t][1] = nxt[t][1];
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);   // this wave's part of the next stage landed
+      __syncthreads();                  // ... and everyone's; stage st may be overwritten next
     }
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's part of the next stage landed
-    __syncthreads();                  // ... and everyone's; stage st may be overwritten next
   }
 
 #pragma unroll
