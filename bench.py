@@ -178,17 +178,23 @@ def step_record_pattern(kernel: str) -> str | None:
     return f'gemv_flat_kernelILi{m.group(1)}ELi{m.group(2)}ELNS0_4WFmtE{fmt}ELNS0_5XModeE{mode}E'
 
 
-def in_step_us(step_times: dict, patterns: tuple, launches_per_step: int) -> float | None:
+def in_step_us(step_times: dict, patterns: tuple, launches_per_step: int, own_us: float | None = None) -> float | None:
     """Summed per-launch device time of the kernels whose records contain
     each of `patterns` (one kernel per pattern, each launched
     `launches_per_step` times per step), or None when any is missing or
-    launched a different number of times."""
+    launched a different number of times, or when the sum lies outside
+    0.5-2x `own_us` (the same kernels timed in a graph of their own
+    launches; inside the step they ran 1.0-1.3x that).  Under an outside
+    profiler (rocprofv3) the records come back with the right counts but
+    durations of about 1 us, which the bound rejects."""
     total = 0.0
     for pat in patterns:
         hits = [v for name, v in step_times.items() if pat in name]
         if len(hits) != 1 or abs(hits[0]['per_step'] - launches_per_step) > 0.01:
             return None
         total += hits[0]['us']
+    if own_us is not None and not 0.5 * own_us <= total <= 2.0 * own_us:
+        return None
     return total
 
 
@@ -643,7 +649,7 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
             pats = ('lm_head_kernel', 'lm_head_pick_kernel')
         else:
             pats = (step_record_pattern(e['kernel']),)
-        us = in_step_us(step_times, pats, e['launches_per_token']) if step_times and all(pats) else None
+        us = in_step_us(step_times, pats, e['launches_per_token'], e['kernel_us']) if step_times and all(pats) else None
         if us is not None:
             e['in_step_us'] = round(us, 3)
             e['in_step_frac'] = round(e['bytes'] / us / 1e3 / HBM_PEAK_GBS, 4)
@@ -657,7 +663,7 @@ def kernel_sections(torch, native, model, runtime, cfg, args, device, capacity: 
     if 'in_step_us' in dom:
         avg_us, timing = dom['in_step_us'], f'kernel: device records over {PROFILED_STEPS} decode steps'
     else:
-        avg_us, timing = dom['kernel_us'], dom['timing'] + ': one-op graph'
+        avg_us, timing = dom['kernel_us'], dom['timing'] + ': one-op graph (no usable in-step records)'
     achieved = dom['bytes'] / avg_us / 1e3
     result['roofline'] = {
         'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',

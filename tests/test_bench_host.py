@@ -72,3 +72,15 @@ def test_in_step_time_is_none_when_the_records_do_not_fit():
     two[GEMV.format(nb=10, mm=1, f=0, x=1) + 'clone'] = {'us': 1.0, 'per_step': 40.0}
     assert bench.in_step_us(two, (gu,), 40) is None            # ambiguous: two records match
     assert bench.in_step_us(RECORDS, ('decode_attention_kernel', 'missing_kernel'), 40) is None
+
+
+def test_in_step_time_is_bounded_by_the_kernels_own_time():
+    """Records with the right counts but implausible durations (what the
+    profiler returns under rocprofv3: about 1 us per launch) are rejected
+    against the kernel's own one-op-graph time; plausible ones pass."""
+    gu = bench.step_record_pattern('gemv_flat_kernel<10, 1, W4, RmsNorm>')
+    assert bench.in_step_us(RECORDS, (gu,), 40, own_us=19.2) == pytest.approx(18.1)
+    assert bench.in_step_us(RECORDS, (gu,), 40, own_us=14.0) == pytest.approx(18.1)   # 1.3x: the step's interleaving
+    broken = {k: {'us': 1.3, 'per_step': v['per_step']} for k, v in RECORDS.items()}
+    assert bench.in_step_us(broken, (gu,), 40, own_us=21.5) is None
+    assert bench.in_step_us(RECORDS, (gu,), 40, own_us=8.0) is None                   # more than 2x
