@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: Qwen3-14B-shaped AWQ-INT4 (W4A16, G=128) decode on one MI355X.
 
-Headline (the workload the metric's published number is
+Headline (the benchmark configs[4], the workload the metric's published number is
 quoted on): batch 1, a 4096-token random prompt, greedy decode with the fp16
 KV cache resident, random-init weights of the Qwen3-14B architecture (40
 layers, hidden 5120, 40/8 heads of 128, SwiGLU 17408, vocab 151936), the
@@ -69,7 +69,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = 'Qwen3-14B AWQ-INT4 decode tok/s at B=1; W4A16 GEMV % of HBM peak'
-PUBLISHED_TOKS = 26.358          # AWQ INT4 G=128 + vLLM Marlin, RTX 3090, same workload
+PUBLISHED_TOKS = 26.358          # the reference's published AWQ INT4 G=128 + vLLM Marlin figure, RTX 3090, same workload
 # Peak allocated GiB the reference publishes for the same runs (README.md:31-32).
 REFERENCE_PEAK_GIB = {'w4': 9.260, 'int8': 15.517}
 HBM_PEAK_GBS = 8000.0

@@ -3,7 +3,7 @@
 Bars: repack/unpack/decode/quantize bit-exact; linear outputs within
 max|d| <= 1e-2 * ||y_ref||_inf, mean|d|/mean|y_ref| <= 2e-3 (fp32
 accumulation), cosine >= 0.9999 and rel-L2 <= 0.02 (``oracle.qdq.parity_ok``).
-Full BASELINE shapes are checked whole at M=1 and on sampled activation rows
+The benchmark configs' full shapes are checked whole at M=1 and on sampled activation rows
 at M=4096 (the oracle restricted to those rows is the same computation).
 """
 import json
