@@ -339,8 +339,9 @@ class DecodeStepGraph:
     (W8A16) weights alike; other formats (W8A8) take the same
     steps with the norms, residual adds and SiLU*up as separate kernels.
     Inputs are the token id and the position (device
-    scalars); the token's embedding row comes from the table in pinned host
-    memory (``wq_embed_rows``); every launch is a HIP kernel of this library,
+    scalars; the step advances the position itself, a torch add at its end);
+    the token's embedding row comes from the table in pinned host memory
+    (``wq_embed_rows``); every other launch is a HIP kernel of this library,
     except that the LM head falls back to torch's GEMM when the hidden size
     is not a multiple of 512."""
 
@@ -355,6 +356,14 @@ class DecodeStepGraph:
         hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         hidden = cfg.hidden_size
         f16 = dict(dtype=torch.float16, device=dev)
+        # The logits and the greedy token share one buffer, so that one copy
+        # hands both to the caller.
+        vocab = cfg.vocab_size
+        tok_off = (2 * vocab + 15) // 16 * 16
+        self.out_buf = torch.zeros(tok_off + 16, dtype=torch.uint8, device=dev)
+        self._vocab, self._tok_off = vocab, tok_off
+        self.logits = self.out_buf[:2 * vocab].view(torch.float16).view(1, vocab)
+        self.next_token = self.out_buf[tok_off:tok_off + 8].view(torch.long)
         self.token = torch.zeros(1, dtype=torch.long, device=dev)
         self.position = torch.zeros(1, dtype=torch.int32, device=dev)
         self.hidden = torch.empty(1, hidden, **f16)
@@ -364,8 +373,6 @@ class DecodeStepGraph:
         self.delta = torch.empty(1, hidden, **f16)
         self.gate_up = torch.empty(1, 2 * cfg.intermediate_size, **f16)
         self.act = torch.empty(1, cfg.intermediate_size, **f16)
-        self.logits = torch.empty(1, cfg.vocab_size, **f16)
-        self.next_token = torch.zeros(1, dtype=torch.long, device=dev)
         self.lm_w4 = model.lm_head_w4
         self.argmax_ws = torch.zeros(_native.argmax_f16_workspace_size(cfg.vocab_size), dtype=torch.uint8,
                                      device=dev) if self.lm_w4 is not None else None
@@ -403,6 +410,8 @@ class DecodeStepGraph:
             self._step()
         torch.cuda.synchronize(dev)
         ops.calls, ops.gemm_calls, model.compute_stats.linear_calls = calls   # set-up launches are not calls
+        # The position the device holds for the next step (None: unknown).
+        self._dev_position = None
 
     def _linear(self, x: Tensor, weights: Mapping, name: str, out: Tensor) -> None:
         prepared = weights[name.removesuffix('.weight') + '._prepared']
@@ -413,6 +422,7 @@ class DecodeStepGraph:
             self._step_fused()
         else:
             self._step_unfused()
+        self.position.add_(1)   # the next token's position, unless the caller asks for another
 
     @staticmethod
     def _fused_linear(x: Tensor, p, **kw) -> None:
@@ -492,19 +502,29 @@ class DecodeStepGraph:
         _native.add_rmsnorm(self.hidden, self.model.final_norm, eps, delta=self.delta, out=self.states)
         self._lm_head()
 
-    def run(self, token: Tensor, position: int) -> Tensor:
+    def run(self, token: Tensor, position: int) -> tuple[Tensor, Tensor]:
+        """One decode step: the token's logits ``[1, 1, vocab]`` and its
+        greedy next token ``[1, 1]``, fresh tensors (one copy of the step's
+        output buffer).  The step advances the device position itself, so the
+        position is written only when it differs from the one the previous
+        replay left there."""
         if not 0 <= position < self.max_seq_len:
             raise ValueError(f'KV cache capacity exceeded: requested {position + 1}, capacity {self.max_seq_len}')
         self.token.copy_(token.reshape(1), non_blocking=True)
-        self.position.fill_(position)
+        if position != self._dev_position:
+            self.position.fill_(position)
         self.graph.replay()
+        self._dev_position = position + 1
         backend = self.model.linear_backend
         if backend is not None:
             backend.calls += 4 * len(self.layers)       # fused QKV, o, fused gate_up, down per layer
             backend.gemm_calls += 4 * len(self.layers)
         else:   # INT8 v1: the reference counts its 7 linears per layer
             self.model.compute_stats.linear_calls += 7 * len(self.layers)
-        return self.logits
+        out = self.out_buf.clone()
+        logits = out[:2 * self._vocab].view(torch.float16).view(1, 1, self._vocab)
+        next_token = out[self._tok_off:self._tok_off + 8].view(torch.long).view(1, 1)
+        return logits, next_token
 
 
 class QuantizedQwen3ForCausalLM:
@@ -644,10 +664,9 @@ class QuantizedQwen3ForCausalLM:
             past = cache.get_seq_length(0)
             if any(n != past for n in cache.lengths):
                 raise RuntimeError('decode graph needs every layer of the cache at the same length')
-            logits = graph.run(input_ids.to(self.device), past)
+            logits, next_token = graph.run(input_ids.to(self.device), past)
             cache.lengths[:] = [past + 1] * len(cache.lengths)
-            return CausalLMOutput(logits=logits.view(1, 1, -1).clone(), cache=cache,
-                                  next_token=graph.next_token.view(1, 1).clone())
+            return CausalLMOutput(logits=logits, cache=cache, next_token=next_token)
 
         ids_cpu = input_ids.detach().to(device='cpu')
         hidden_cpu = F.embedding(ids_cpu, self.store.embed_tokens)

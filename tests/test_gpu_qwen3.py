@@ -139,6 +139,37 @@ def test_graph_decode_equals_eager_decode(tiny):
         ta = la[:, -1].argmax(-1, keepdim=True)
 
 
+def test_pooled_graph_restarts_at_the_new_caches_position(tiny):
+    """The decode step advances its device position itself, and the host
+    writes the position only when the next call asks for another one: a
+    pooled graph handed to a new cache (the previous owner gone) left the
+    device at the old cache's next position, and the new cache's steps must
+    still match the eager decoder at its own positions."""
+    import gc
+    np_model, model, _ = tiny
+    eager, _ = build(np_model, TinyCfg, decode_graph=False)
+    ca = model.make_resident_cache(batch_size=1, max_seq_len=160)
+    graph = ca._decode_graph
+    t = model(torch.arange(20, 50)[None].cuda(), cache=ca, logits_to_keep=1).logits[:, -1].argmax(-1, keepdim=True)
+    for _ in range(3):
+        t = model(t, cache=ca).logits[:, -1].argmax(-1, keepdim=True)
+    assert graph._dev_position == 33                  # positions 30, 31, 32 decoded
+    del ca
+    gc.collect()
+    cb = model.make_resident_cache(batch_size=1, max_seq_len=160)
+    assert cb._decode_graph is graph
+    ce = eager.make_resident_cache(batch_size=1, max_seq_len=160)
+    prompt = torch.arange(100, 110)[None].cuda()
+    tb = model(prompt, cache=cb, logits_to_keep=1).logits[:, -1].argmax(-1, keepdim=True)
+    te = eager(prompt, cache=ce, logits_to_keep=1).logits[:, -1].argmax(-1, keepdim=True)
+    assert torch.equal(tb, te)
+    for step in range(3):
+        lb, le = model(tb, cache=cb).logits, eager(tb, cache=ce).logits
+        _ok(lb[0], le[0].float().cpu().numpy(), f'pooled graph vs eager, step {step}')
+        assert graph._dev_position == 11 + step
+        tb = lb[:, -1].argmax(-1, keepdim=True)
+
+
 def test_greedy_generate_runs_the_reference_loop(tiny):
     from ondeviceinfer_amd.generation import greedy_generate
     np_model, model, _ = tiny
