@@ -417,7 +417,6 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
   constexpr int kLoadsPerBlock = kInstrPerWave + (F == GFmt::W4 ? 3 : 2) * NT;
   static_assert(D >= 3 && (D - 2) * kLoadsPerBlock <= 63, "ring depth");
   __shared__ __attribute__((aligned(1024))) uint8_t xs[D * kStageBytes];
-  __shared__ uint32_t arrival;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -546,9 +545,15 @@ __global__ __launch_bounds__(256) void wq_gemm_deep_kernel(const half_t* __restr
     __builtin_amdgcn_s_waitcnt(0);   // this wave's partials are acknowledged
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();    // ... and every wave's
-    if (tid == 0) arrival = __hip_atomic_fetch_add(&ws_cnt[tile_id], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The arrival count goes through the first word of the activation ring,
+    // dead once every wave has passed the barrier above (its run-out copies
+    // landed before each wave's vmcnt(0)): a separate LDS word would push
+    // the five-stage 64-row ring (80 KiB) past half of the CU's LDS and halve
+    // its occupancy.
+    uint32_t* arrival = reinterpret_cast<uint32_t*>(xs);
+    if (tid == 0) *arrival = __hip_atomic_fetch_add(&ws_cnt[tile_id], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (arrival != (uint32_t)(S - 1)) return;
+    if (*arrival != (uint32_t)(S - 1)) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -635,7 +640,10 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
 // covers the machine twice over.  Otherwise W4 takes the most work per
 // workgroup that still gives at least 384 workgroups: 128-wide slices of
 // 64-row tiles (NT = 2, MT = 4), then 64-wide slices (NT = 1), then 64-wide
-// slices of 32-row tiles on the deep ring (NT = 1, MT = 2, D = 6).  The
+// slices of 32-row tiles on the deep ring (NT = 1, MT = 2, D = 4: three
+// blocks in flight; D = 6 was 2-15 % slower once the block math ran at raised
+// priority, e.g. 5120^2 at M = 65 17.4 against 20.4 us, q/o at M = 128 23.5
+// against 25.0 us, same bits).  The
 // narrow shapes gain most (k_proj 5120->1024: M = 2048 46.7 -> 38.0 us,
 // M = 512 37.4 -> 21.8 us; down 17408->5120 at M = 128 101 -> 77 us; 5120^2
 // at M = 2048 155 -> 127 us).  INT8 tiles take the same grids (5120^2 at
@@ -663,7 +671,7 @@ int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* m
       return launch_gemm<F, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
     if (((ntile + 3) / 4) * mb64 >= kMinGrid)
       return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
-    return launch_gemm_deep<F, 1, 2, 6>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled, ws, ws_bytes);
+    return launch_gemm_deep<F, 1, 2, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled, ws, ws_bytes);
   } else {
     if (M <= 256) return launch_gemm<F, 1, 4>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
     return launch_gemm<F, 1, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
@@ -731,8 +739,11 @@ int launch_w8_gemm_epi(const half_t* x, int M, int K, const int8_t* tiles, const
   }
 }
 
-// Wide N at 16 < M <= 64: the deep ring keeps five weight blocks per wave in
-// flight where the prefill GEMM keeps one.  Two tiles per wave when that still
+// Wide N at 16 < M <= 64: the deep ring keeps three weight blocks per wave in
+// flight where the prefill GEMM keeps one (at M <= 32 a ring of five measured
+// 4-5 % slower on the fused gate_up and 1-3 % on the LM head; at M = 40 and 64
+// four stages of 64-row tiles (64 KiB) run 45.6 / 48.4 us on the fused gate_up
+// where five (80 KiB) fit only one workgroup per CU, same bits).  Two tiles per wave when that still
 // leaves more than 1024 workgroups (the LM head), else one (the fused
 // gate_up).  Measured at K = 5120: gate_up 46.8 -> 39.9 us (M = 32) and
 // 85.1 -> 50.2 us (M = 64), LM head 153.7 -> 106.8 us and 242.7 -> 148.8 us.
@@ -743,10 +754,10 @@ int launch_w4_gemm_small(const half_t* x, int M, int K, const uint4_t* tiles, co
   const int bpg = G / kW4BlockK;
   const int ntile = (N + 15) / 16;
   if (M <= 32) {
-    if (ntile >= 4096) return launch_gemm_deep<GFmt::W4, 2, 2, 6>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
-    return launch_gemm_deep<GFmt::W4, 1, 2, 6>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
+    if (ntile >= 4096) return launch_gemm_deep<GFmt::W4, 2, 2, 4>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
+    return launch_gemm_deep<GFmt::W4, 1, 2, 4>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
   }
-  return launch_gemm_deep<GFmt::W4, 2, 4, 5>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
+  return launch_gemm_deep<GFmt::W4, 2, 4, 4>(x, M, K, tiles, meta, N, bpg, nullptr, y, s, 0);
 }
 
 int launch_w8_gemm(const half_t* x, int M, int K, const int8_t* q, const half_t* scale, const half_t* bias, int N,
