@@ -636,8 +636,16 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
   return check_launch(F == GFmt::W4 ? "w4_gemm_deep" : "w8_gemm_deep");
 }
 
-// Grids: 256-wide n slices of 128-row tiles (NT = 4, MT = 8) when that still
-// covers the machine twice over.  Otherwise W4 takes the most work per
+// Workgroups from which the prefill GEMM takes 256-wide n slices of 128-row
+// tiles (NT = 4, MT = 8): 384, three quarters of the 512 resident slots (the
+// 128-row grid at 448 workgroups ran the fused QKV at M = 2048 in 137 us
+// against 155 us for 64-row tiles, 5120^2 at M = 3072 (480) in 143 against
+// 171 us, down 458 against 565 us; at 320, 5120^2 at M = 2048, the 64-row
+// grid stays ahead, 118 against 129 us; same bits on every grid).
+constexpr long kWideGrid = 384;
+
+// Grids: 256-wide n slices of 128-row tiles (NT = 4, MT = 8) from kWideGrid
+// workgroups on.  Otherwise W4 takes the most work per
 // workgroup that still gives at least 384 workgroups: 128-wide slices of
 // 64-row tiles (NT = 2, MT = 4), then 64-wide slices (NT = 1), then 64-wide
 // slices of 32-row tiles on the deep ring (NT = 1, MT = 2, D = 4: three
@@ -653,7 +661,7 @@ int launch_gemm_deep(const half_t* x, int M, int K, const void* w, const void* m
 // Whether launch_gemm_auto runs the deep ring on 32-row tiles for this shape.
 bool gemm_takes_deep(long M, long N, bool w4_or_tiles) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128, mb64 = (M + 63) / 64;
-  if (((ntile + 15) / 16) * mblk >= 512 || !w4_or_tiles) return false;
+  if (((ntile + 15) / 16) * mblk >= kWideGrid || !w4_or_tiles) return false;
   constexpr long kMinGrid = 384;
   return ((ntile + 7) / 8) * mb64 < kMinGrid && ((ntile + 3) / 4) * mb64 < kMinGrid;
 }
@@ -663,7 +671,7 @@ int launch_gemm_auto(const half_t* x, int M, int K, const void* w, const void* m
                      const half_t* bias, half_t* y, hipStream_t s, int w8_tiled, void* ws = nullptr,
                      size_t ws_bytes = 0) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128;
-  if (((ntile + 15) / 16) * mblk >= 512) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
+  if (((ntile + 15) / 16) * mblk >= kWideGrid) return launch_gemm<F, 4, 8>(x, M, K, w, meta, N, bpg, bias, y, s, w8_tiled);
   if (F == GFmt::W4 || w8_tiled) {
     constexpr long kMinGrid = 384;
     const long mb64 = (M + 63) / 64;
@@ -701,7 +709,7 @@ size_t w4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 int gemm_epi_plan(int64_t M, int64_t N, int64_t K, int mode, int64_t block_bytes) {
   const long ntile = (N + 15) / 16, mblk = (M + 127) / 128, mb64 = (M + 63) / 64;
   int plan = 0;
-  if (((ntile + 15) / 16) * mblk >= 512) plan = 1;
+  if (((ntile + 15) / 16) * mblk >= kWideGrid) plan = 1;
   else if (((ntile + 7) / 8) * mb64 >= 384) plan = 2;
   else if (((ntile + 3) / 4) * mb64 >= 384) plan = 3;
   if (mode == 1) {
