@@ -60,6 +60,24 @@ def test_w4a16_gemm_odd_block_counts(gpu, n, k, m):
     assert np.array_equal(y_short.view(np.uint16), y[:70].view(np.uint16))
 
 
+def test_w4a16_gemm_long_k_split_on_a_wider_grid(gpu):
+    """k = 8320 (65 blocks, at least 64: a long chain) on the deep ring's
+    352 workgroups (16 n slices x 22 row blocks at m = 700), above the 320
+    to which short chains split: four k splits of 16 or 17 blocks."""
+    n, k, m = 1000, 8320, 700
+    assert _native.w4a16_workspace_size(m, n, k, 128) > 0
+    assert _native.w4a16_workspace_size(m, n, 5120, 128) == 0     # a short chain on the same grid
+    name = 'p.weight'
+    weights, x = synth.w4_case(n, k, m, seed=7, name=name)
+    layer = {key: dev(v, gpu) for key, v in weights.items()}
+    backend = wq.CompressedLinearBackend('marlin')
+    backend.prepare(layer, name)
+    print(f'[w4 gemm long-k split] n={n} k={k} m={m}', flush=True)
+    y = host(backend.linear(dev(x, gpu), layer, name))
+    rows = np.sort(np.random.default_rng(m).choice(m, size=48, replace=False))
+    check_parity(y[rows], qdq.qdq_linear(x[rows], weights, name), f'w4 long-k n={n} k={k} m={m}')
+
+
 @pytest.mark.parametrize('n,k,m', [(1000, 384, 200), (1040, 640, 300), (5120, 640, 1100)])
 def test_w8a16_gemm_odd_block_counts(gpu, n, k, m):
     _, q, s, x = synth.int8_case(n, k, m, seed=n + k + m)
