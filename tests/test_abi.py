@@ -58,3 +58,21 @@ def test_status_maps_to_python_exceptions():
         _native.w4_repack_size(12, 256, 128)
     assert _native.w4_repack_size(16, 256, 128) == (16 * 128, 2 * 40)
     assert _native.w4a16_workspace_size(1, 5120, 5120, 128) == 0
+
+
+def test_prefill_k_split_workspace_follows_the_chain_length():
+    """The deep-ring GEMM's k split, as the host sizes its workspace (no GPU
+    needed): a 16 KiB counter region plus one fp32 partial tile set of
+    4 waves x NT x MT KiB per (workgroup, split), NT = 1 and MT = 2 (32-row
+    tiles) at these M.  Short chains (40 blocks) split only grids of at
+    most 320 workgroups, long ones (64 blocks or more) up to 640."""
+    counters, per_split_tile = 16384, 4 * 1 * 2 * 1024
+    # down 17408->5120 (136 blocks): 80 n slices x 4 / 8 row blocks
+    assert _native.w4a16_workspace_size(128, 5120, 17408, 128) == counters + 320 * 4 * per_split_tile
+    assert _native.w4a16_workspace_size(256, 5120, 17408, 128) == counters + 640 * 2 * per_split_tile
+    # q/o 5120->5120 (40 blocks) at M = 256: 640 workgroups keep the whole k range
+    assert _native.w4a16_workspace_size(256, 5120, 5120, 128) == 0
+    # 65 blocks, 16 n slices x 22 row blocks = 352 workgroups: four splits
+    assert _native.w4a16_workspace_size(700, 1000, 8320, 128) == counters + 352 * 4 * per_split_tile
+    # M = 257: 64-row tiles (400 workgroups), no deep ring, no split
+    assert _native.w4a16_workspace_size(257, 5120, 17408, 128) == 0
