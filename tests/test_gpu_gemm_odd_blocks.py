@@ -78,6 +78,31 @@ def test_w4a16_gemm_long_k_split_on_a_wider_grid(gpu):
     check_parity(y[rows], qdq.qdq_linear(x[rows], weights, name), f'w4 long-k n={n} k={k} m={m}')
 
 
+def test_w4a16_down_shape_splits_k_at_m256(gpu):
+    """The down projection's shape (17408 -> 5120, 136 blocks) at M = 256:
+    640 deep-ring workgroups in two k splits of 68 blocks, against the oracle
+    on 48 rows, and against the whole-k call (a workspace too small for the
+    split) to the same bar; the split's counters are back at zero."""
+    n, k, m = 5120, 17408, 256
+    nbytes = _native.w4a16_workspace_size(m, n, k, 128)
+    assert nbytes == 16384 + 640 * 2 * 8192
+    name = 'mlp.down_proj.weight'
+    weights, x = synth.w4_case(n, k, m, seed=11, name=name)
+    layer = {key: dev(v, gpu) for key, v in weights.items()}
+    wq.CompressedLinearBackend('marlin').prepare(layer, name)
+    prep = layer['mlp.down_proj._prepared']
+    xd = dev(x, gpu)
+    print(f'[w4 gemm down shape split] n={n} k={k} m={m}', flush=True)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    split = host(_native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128, workspace=ws))
+    whole = host(_native.w4a16_linear(xd, prep.tiles, prep.meta, n, 128,
+                                      workspace=torch.zeros(16, dtype=torch.uint8, device=gpu)))
+    rows = np.sort(np.random.default_rng(m).choice(m, size=48, replace=False))
+    check_parity(split[rows], qdq.qdq_linear(x[rows], weights, name), 'down shape, two k splits')
+    check_parity(split, whole.astype(np.float32), 'down shape, split against whole k')
+    assert torch.count_nonzero(ws[:16384]).item() == 0
+
+
 @pytest.mark.parametrize('n,k,m', [(1000, 384, 200), (1040, 640, 300), (5120, 640, 1100)])
 def test_w8a16_gemm_odd_block_counts(gpu, n, k, m):
     _, q, s, x = synth.int8_case(n, k, m, seed=n + k + m)
