@@ -591,7 +591,7 @@ int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, 
   return check_launch(F == GFmt::W4 ? "w4_gemm" : "w8_gemm");
 }
 
-// k splits of the deep-ring grid (W4) for grids of at most 320 workgroups
+// k splits of the deep-ring grid (W4) for grids of at most 384 workgroups
 // (640 on long k chains):
 // enough workgroups to cover the machine several times (at most 2048 with
 // the splits) while every split keeps at least 8 blocks; 1 when the
@@ -599,10 +599,12 @@ int launch_gemm(const half_t* x, int M, int K, const void* w, const void* meta, 
 // (5120->1024) M = 65 / 128 / 300 22.8 / 22.5 / 23.1 -> 11.4 / 11.8 / 16.2;
 // q/o M = 65 / 128 22.9 / 27.0 -> 20.6 / 24.9; down (17408->5120) M = 65 /
 // 128 68.7 / 79.9 -> 49.0 / 59.5.  Larger grids lost: fused QKV M = 128
-// (448 workgroups) 29.2 -> 32.8, q/o M = 256 35.5 -> 37.6.  Long k chains
+// (448 workgroups) 29.2 -> 32.8, q/o M = 256 35.5 -> 37.6; up to 384 gained
+// (320 before): fused QKV M = 65 / 96 (336 workgroups) 24.5 / 25.2 -> 23.2 /
+// 24.1, k/v M = 700 / 760 25.5 / 25.8 -> 23.9 / 24.7.  Long k chains
 // (at least 64 blocks) split up to 640 workgroups: down at M = 256 (640
 // workgroups, two splits of 68 blocks) 101.6 -> 94.9.
-constexpr long kDeepSplitMaxGrid = 320;
+constexpr long kDeepSplitMaxGrid = 384;
 constexpr long kDeepSplitMaxGridLongK = 640;
 constexpr int kDeepLongKBlocks = 64;
 

@@ -65,12 +65,17 @@ def test_prefill_k_split_workspace_follows_the_chain_length():
     needed): a 16 KiB counter region plus one fp32 partial tile set of
     4 waves x NT x MT KiB per (workgroup, split), NT = 1 and MT = 2 (32-row
     tiles) at these M.  Short chains (40 blocks) split only grids of at
-    most 320 workgroups, long ones (64 blocks or more) up to 640."""
+    most 384 workgroups, long ones (64 blocks or more) up to 640."""
     counters, per_split_tile = 16384, 4 * 1 * 2 * 1024
     # down 17408->5120 (136 blocks): 80 n slices x 4 / 8 row blocks
     assert _native.w4a16_workspace_size(128, 5120, 17408, 128) == counters + 320 * 4 * per_split_tile
     assert _native.w4a16_workspace_size(256, 5120, 17408, 128) == counters + 640 * 2 * per_split_tile
     # q/o 5120->5120 (40 blocks) at M = 256: 640 workgroups keep the whole k range
+    assert _native.w4a16_workspace_size(256, 5120, 5120, 128) == 0
+    # fused QKV 5120->7168 (40 blocks): 112 n slices x 3 row blocks at M = 65 split
+    # in four; 4 row blocks at M = 128 (448 workgroups) keep the whole k range
+    assert _native.w4a16_workspace_size(65, 7168, 5120, 128) == counters + 336 * 4 * per_split_tile
+    assert _native.w4a16_workspace_size(128, 7168, 5120, 128) == 0
     assert _native.w4a16_workspace_size(256, 5120, 5120, 128) == 0
     # 65 blocks, 16 n slices x 22 row blocks = 352 workgroups: four splits
     assert _native.w4a16_workspace_size(700, 1000, 8320, 128) == counters + 352 * 4 * per_split_tile

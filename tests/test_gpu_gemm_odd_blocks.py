@@ -62,9 +62,9 @@ def test_w4a16_gemm_odd_block_counts(gpu, n, k, m):
 
 def test_w4a16_gemm_long_k_split_on_a_wider_grid(gpu):
     """k = 8320 (65 blocks, at least 64: a long chain) on the deep ring's
-    352 workgroups (16 n slices x 22 row blocks at m = 700), above the 320
+    464 workgroups (16 n slices x 29 row blocks at m = 900), above the 384
     to which short chains split: four k splits of 16 or 17 blocks."""
-    n, k, m = 1000, 8320, 700
+    n, k, m = 1000, 8320, 900
     assert _native.w4a16_workspace_size(m, n, k, 128) > 0
     assert _native.w4a16_workspace_size(m, n, 5120, 128) == 0     # a short chain on the same grid
     name = 'p.weight'
